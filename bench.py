@@ -1,0 +1,267 @@
+"""Batch-1 decode benchmark on one MI355X (kernel lines for configs 1-4).
+
+    python bench.py [--gpus 1] [--steps 256] [--warmup 16] [--dtypes bf16,int8,int4] [--no-cpu]
+
+A "step" is one batch-1 decode step (one token) of a seeded random-init Llama-3.2-1B-shaped model:
+16 layers, hidden 2048, FFN 8192, vocab 128256, GQA 32/8, tied embeddings, weights N(0, 0.02)
+(bf16 master; int8 per-row and int4 group-128 files quantised from it).  Per weight type: a 16-token
+seeded prompt, W untimed warm-up decode steps, then K greedy decode steps timed with the device
+drained on both sides; each step is one replay of the captured hipGraph with the token fed back on
+the device (no host sync inside the timed region, as reference src/tools/cudallm_bench.cpp:64-80).
+
+Printed last, on one line: the JSON record.  ``value`` is bf16 decode tok/s; ``decode`` holds all
+three weight types; ``roofline`` is the dominant kernel (the fused RMSNorm + gate_up + SwiGLU
+matvec, 16 launches per token) timed live with HIP events on the launching stream over rotating
+weight copies (> 1 GiB, so the 256 MB Infinity Cache cannot serve them); ``cpu_baseline`` is the
+CPU oracle (the reference's algorithm restated, oracle/model.py) timed on this host.
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import tempfile
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "batch-1 decode tok/s (bf16/int8/int4) + matvec HBM GB/s as % of peak"
+PEAK_HBM = 8.0e12  # MI355X HBM3E, bytes/s
+PROMPT = 16
+KV_BYTES_PER_POS = 16 * 2 * 8 * 64 * 2  # layers x (K,V) x kv heads x head_dim x fp16
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def prompt_ids(n: int) -> list[int]:
+    rng = np.random.default_rng(16)
+    return [128000] + [int(t) for t in rng.integers(0, 128256, n - 1)]
+
+
+def bench_decode(path, wd: str, steps: int, warmup: int, torch) -> dict:
+    from cudallm_amd import engine as E
+    t_load = time.perf_counter()
+    with E.Engine(path) as eng:
+        load_s = time.perf_counter() - t_load
+        weight_bytes = eng.config["weight_bytes"]
+        ids = prompt_ids(PROMPT)
+        eng.reset()
+        for t in ids:
+            eng.step_async(t)
+        for _ in range(warmup):
+            eng.step_async(None)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            eng.step_async(None)
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+        nxt, _ = eng.step(None)
+    ctx0 = PROMPT + warmup
+    kv = KV_BYTES_PER_POS * (ctx0 + (steps + 1) // 2)  # reference cudallm_bench.cpp:82-85 accounting
+    bpt = weight_bytes + kv
+    tok_s = steps / dt
+    return {"tok_s": tok_s, "ms_per_token": 1e3 * dt / steps, "weight_bytes": weight_bytes, "bytes_per_token": bpt,
+            "gbps": bpt * tok_s / 1e9, "frac_of_8tbs": bpt * tok_s / PEAK_HBM,
+            "roofline_tok_s": PEAK_HBM / bpt, "context": [ctx0, ctx0 + steps], "load_s": round(load_s, 2),
+            "last_token": nxt}
+
+
+SHAPES = [("qkv", 3072, 2048, "store", True), ("wo", 2048, 2048, "add", False),
+          ("gate_up", 16384, 2048, "swiglu", True), ("down", 2048, 8192, "add", False),
+          ("lm_head", 128256, 2048, "store", True)]
+
+
+def matvec_bytes(wd: str, rows: int, cols: int) -> int:
+    """Algorithmic HBM bytes of one launch: weights + scales (x and y are < 0.1 %)."""
+    n = rows * cols
+    if wd == "bf16":
+        return 2 * n
+    if wd == "int8":
+        return n + 4 * rows
+    return n // 2 + 2 * rows * (cols // 128)
+
+
+def bench_matvec(wd: str, name: str, rows: int, cols: int, ep: str, norm: bool, iters: int, torch,
+                 rpb: int = 0) -> dict:
+    """Median-free live timing: HIP events on torch's current stream around `iters` launches that
+    rotate over enough weight copies to exceed 1 GiB."""
+    from cudallm_amd import engine as E
+    dev = torch.device("cuda")
+    nbytes = matvec_bytes(wd, rows, cols)
+    copies = max(2, math.ceil((1 << 30) * 1.5 / nbytes))
+    g = torch.Generator(device=dev)
+    g.manual_seed(rows + cols)
+    ws, ss = [], []
+    for _ in range(copies):
+        if wd == "bf16":
+            ws.append((torch.randn(rows, cols, device=dev, generator=g) * 0.02).to(torch.bfloat16))
+            ss.append(None)
+        elif wd == "int8":
+            ws.append(torch.randint(-127, 128, (rows, cols), device=dev, dtype=torch.int8, generator=g))
+            ss.append(torch.rand(rows, device=dev, generator=g) * 0.01 + 0.005)
+        else:
+            ws.append(torch.randint(0, 256, (rows, cols // 2), device=dev, dtype=torch.uint8, generator=g))
+            ss.append((torch.rand(rows, cols // 128, device=dev, generator=g) * 0.01 + 0.005).half())
+    x = torch.randn(cols, device=dev)
+    nw = torch.rand(cols, device=dev) + 0.5
+    out_rows = rows // 2 if ep == "swiglu" else rows
+    y = torch.zeros(out_rows, device=dev)
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+
+    def launch(i):
+        w, s = ws[i % copies], ss[i % copies]
+        E.launch_matvec(wd, ep, rpb, w.data_ptr(), s.data_ptr() if s is not None else None, x.data_ptr(),
+                        nw.data_ptr() if norm else None, 1e-5, y.data_ptr(), rows, cols, sp)
+
+    for i in range(min(copies, 20)):
+        launch(i)
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for i in range(iters):
+        launch(i)
+    stop.record(stream)
+    stop.synchronize()
+    us = start.elapsed_time(stop) * 1e3 / iters
+    del ws, ss
+    torch.cuda.empty_cache()
+    return {"name": name, "wtype": wd, "rows": rows, "cols": cols, "epilogue": ep, "fuse_norm": norm,
+            "bytes": nbytes, "avg_us": us, "gbps": nbytes / us / 1e3, "frac_of_8tbs": nbytes / us / 1e3 / 8000.0,
+            "copies": copies}
+
+
+def cpu_baseline(path, budget_s: float) -> dict:
+    """The reference's CPU path (restated in oracle/model.py: fp32 dequantise per matmul, fp16 KV
+    cache) decoding the same bf16 model on this host, for about `budget_s` seconds."""
+    import torch
+    from oracle.model import OracleModel
+    cores = min(16, os.cpu_count() or 1)
+    m = OracleModel(path, cache_dense=False, threads=cores)
+    ids = prompt_ids(PROMPT)
+    m.step(ids[0])  # warm-up (page cache, allocator)
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < budget_s and n + 1 < len(ids):
+        m.step(ids[n + 1])
+        n += 1
+    dt = time.perf_counter() - t0
+    return {"value": n / dt, "unit": "tok/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"{n} bf16 decode steps (positions 1..{n}) of the same synthetic model by the oracle "
+                      f"(torch fp32 on the host, weights dequantised per matmul), {dt:.1f} s; "
+                      f"os.cpu_count()={os.cpu_count()}"}
+
+
+def cpu_matvec_config1(reps: int = 20) -> dict:
+    """BASELINE config 1 on the CPU: int8 8192x2048 dequantised to fp32 then W @ x (reference.py:33-37)."""
+    import torch
+    from oracle import quantize as Q
+    rng = np.random.default_rng(1)
+    w = Q.bf16_bits_to_f32(Q.bf16_round_bits(rng.normal(0, 0.02, size=(8192, 2048)).astype(np.float32)))
+    q, s = Q.quantize_int8_rows(w)
+    tq, ts = torch.from_numpy(q), torch.from_numpy(s)
+    x = torch.from_numpy(rng.standard_normal(2048).astype(np.float32))
+    times = []
+    for i in range(reps + 3):
+        t0 = time.perf_counter()
+        _ = (tq.float() * ts[:, None]) @ x
+        if i >= 3:
+            times.append(time.perf_counter() - t0)
+    us = float(np.median(times)) * 1e6
+    return {"us": us, "gbps": 16809984 / us / 1e3, "threads": torch.get_num_threads()}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--dtypes", default="bf16,int8,int4")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-kernels", action="store_true", help="skip the per-shape matvec lines")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--model-dir", default=None)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU only (batch-1 decode does not shard across GPUs here); "
+              "run it with --gpus 1", file=sys.stderr)
+        return 2
+    if PROMPT + args.warmup + args.steps + 1 > 4096:
+        print("bench.py: prompt + warmup + steps must fit the 4096-token context", file=sys.stderr)
+        return 2
+
+    import torch
+    from cudallm_amd import synth
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 1
+    torch.cuda.set_device(0)
+    dtypes = [d for d in args.dtypes.split(",") if d]
+    base = args.model_dir or ("/dev/shm" if os.path.isdir("/dev/shm") else None)
+    tmp = tempfile.TemporaryDirectory(dir=base)
+    paths = {}
+    decode = {}
+    for wd in dtypes:
+        paths[wd] = Path(tmp.name) / f"bench_{wd}.cudallm"
+        t0 = time.perf_counter()
+        synth.write_model(paths[wd], wd, seed=1234)
+        log(f"[bench] wrote {wd} model in {time.perf_counter() - t0:.1f} s")
+        decode[wd] = bench_decode(paths[wd], wd, args.steps, args.warmup, torch)
+        log(f"[bench] decode {wd}: {decode[wd]['tok_s']:.1f} tok/s, {decode[wd]['gbps']:.0f} GB/s "
+            f"({100 * decode[wd]['frac_of_8tbs']:.1f} % of 8 TB/s)")
+        if wd != "bf16" or args.no_cpu:
+            paths[wd].unlink()
+
+    head_wd = "bf16" if "bf16" in dtypes else dtypes[0]
+    dom = bench_matvec(head_wd, "gate_up", 16384, 2048, "swiglu", True, 400, torch)
+    log(f"[bench] gate_up {head_wd} matvec: {dom['avg_us']:.2f} us, {dom['gbps']:.0f} GB/s")
+    matvecs = []
+    if not args.no_kernels:
+        for wd in dtypes:
+            per = {}
+            for name, rows, cols, ep, norm in SHAPES:
+                r = bench_matvec(wd, name, rows, cols, ep, norm, 200 if name != "lm_head" else 50, torch)
+                matvecs.append(r)
+                per[name] = r["avg_us"]
+            weighted = 16 * (per["qkv"] + per["wo"] + per["gate_up"] + per["down"]) + per["lm_head"]
+            matvecs.append({"name": "weighted_us", "wtype": wd, "us": weighted})
+            log(f"[bench] {wd} matvec weighted 16*(qkv+wo+gate_up+down)+lm_head = {weighted:.1f} us")
+
+    cpu = None
+    if not args.no_cpu and "bf16" in paths and paths["bf16"].exists():
+        cpu = cpu_baseline(paths["bf16"], args.cpu_seconds)
+        cpu["matvec_config1_int8"] = cpu_matvec_config1()
+        log(f"[bench] cpu baseline {cpu['value']:.3f} tok/s on {cpu['cores']} threads")
+    tmp.cleanup()
+
+    head = decode[head_wd]
+    rec = {
+        "metric": METRIC, "value": round(head["tok_s"], 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(head["ms_per_token"], 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": head_wd,
+        "data": "synthetic: seeded random-init Llama-3.2-1B-shaped weights N(0,0.02), bf16 master",
+        "config": {"workload": f"batch-1 greedy decode, {head_wd} weights, 16-token prompt + {args.warmup} warm-up "
+                               f"+ {args.steps} timed steps, hipGraph replay (BASELINE config 5)",
+                   "model": "llama-3.2-1b-shaped (random init)", "global_batch": 1,
+                   "seq_len": PROMPT + args.warmup + args.steps, "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "hbm", "achieved": round(dom["gbps"], 1), "peak": 8000.0, "unit": "GB/s",
+                     "frac": round(dom["frac_of_8tbs"], 4), "traffic": None,
+                     "kernel": f"matvec_fast<{head_wd}, SWIGLU, norm> gate_up 16384x2048",
+                     "bytes_per_launch": dom["bytes"], "avg_us": round(dom["avg_us"], 3)},
+        "cpu_baseline": cpu,
+        "decode": {wd: {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
+                   for wd, r in decode.items()},
+        "matvec": [{k: (round(v, 3) if isinstance(v, float) else v) for k, v in r.items()} for r in matvecs],
+    }
+    print(json.dumps(rec), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

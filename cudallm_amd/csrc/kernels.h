@@ -1,0 +1,64 @@
+// Host-side launch functions of the gfx950 kernels.  Each validates the shapes its kernel and
+// grid assume before launching (a wrong shape becomes an ArgError, never a device fault).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "common.h"
+
+namespace cllm {
+
+constexpr int kAttnChunk = 128;    // tokens per split-K attention chunk
+constexpr int kArgmaxParts = 256;  // partial results of the two-pass argmax
+
+struct MatvecArgs {
+    const void* w;
+    const void* scales;
+    const float* x;
+    const float* norm_w;  // non-null when the RMSNorm prologue is fused
+    float eps;
+    float* y;
+    int rows, cols;
+};
+
+int default_rpb(WType wt);
+// y (= | +=) W x^ with the selected epilogue; x^ = rmsnorm(x) * norm_w when norm_w != null.
+void launch_matvec(WType wt, Epilogue ep, const MatvecArgs& a, int rpb, hipStream_t s);
+// One thread per row, bf16, STORE only: the deliberately uncoalesced ablation baseline.
+void launch_matvec_naive(const MatvecArgs& a, hipStream_t s);
+
+void launch_rmsnorm(const float* x, const float* w, float eps, float* y, int n, hipStream_t s);
+void launch_add_inplace(float* x, const float* y, int n, hipStream_t s);
+void launch_silu_mul(const float* gu, float* act, int inter, hipStream_t s);
+void launch_set_token(int* d_token, int token, hipStream_t s);
+void launch_embedding(WType wt, const void* w, const void* scales, const int* d_token, float* x, int hidden,
+                      int vocab, int group_size, hipStream_t s);
+
+// RoPE on the q (and k) heads of qkv = [q(nh*hd) | k(nkv*hd) | v(nkv*hd)] at position *d_pos.
+// fused: q rotated in place, rotated k and v written to the fp16 caches (k in qkv left as is).
+void launch_rope_kv_fused(float* qkv, const float* inv_freq, uint16_t* k_cache, uint16_t* v_cache, const int* d_pos,
+                          int nh, int nkv, int hd, int max_seq, hipStream_t s);
+void launch_rope_inplace(float* qkv, const float* inv_freq, const int* d_pos, int nh, int nkv, int hd, hipStream_t s);
+void launch_kv_write(const float* qkv, uint16_t* k_cache, uint16_t* v_cache, const int* d_pos, int nh, int nkv,
+                     int hd, int max_seq, hipStream_t s);
+
+// Split-K GQA decode attention over ctx = *d_pos + 1 tokens of the fp16 caches [nkv][max_seq][hd].
+void launch_attention_splitk(const float* q, const uint16_t* k_cache, const uint16_t* v_cache, const int* d_pos,
+                             float* part_o, float* part_ml, float* out, int nh, int nkv, int hd, int max_seq,
+                             hipStream_t s);
+void launch_attention_naive(const float* q, const uint16_t* k_cache, const uint16_t* v_cache, const int* d_pos,
+                            float* out, int nh, int nkv, int hd, int max_seq, hipStream_t s);
+
+// Deterministic argmax (ties -> lowest index); writes *d_token and advances *d_pos by one.
+void launch_argmax(const float* logits, int n, float* part_v, int* part_i, int* d_token, int* d_pos, hipStream_t s);
+
+// Weight quantisers (bit-identical to the numpy definitions).
+void launch_quantize_int8_rows(const float* w, int rows, int cols, int8_t* q, float* scales, hipStream_t s);
+void launch_quantize_int4_groups(const float* w, int rows, int cols, uint8_t* packed, uint16_t* scales, hipStream_t s);
+void launch_unpack_int4(const uint8_t* packed, int rows, int cols, int8_t* q, hipStream_t s);
+
+int device_cu_count();
+
+}  // namespace cllm

@@ -1,0 +1,80 @@
+// Device helpers shared by the gfx950 kernels: wave64 reductions built from DPP row operations,
+// streaming 128-bit loads, bf16/fp16 conversions.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace cllm {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+
+// 128-bit load marked non-temporal: weights are read exactly once per decode step, so they
+// should not displace the activations and the KV cache from the caches.
+__device__ __forceinline__ u32x4 load_stream(const void* p) {
+    return __builtin_nontemporal_load(static_cast<const u32x4*>(p));
+}
+
+// DPP move of a float within 16-lane rows (control words of the gfx9 DPP encoding).
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, true));
+}
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;  // lane i <-> 7-i inside each 8
+constexpr int kDppMirror = 0x140;      // lane i <-> 15-i inside each 16
+
+// Sum over all 64 lanes; every lane gets the same result.  Fixed association order, so the
+// result is deterministic: (((row0 + row1) + row2) + row3) of the 16-lane butterfly sums.
+__device__ __forceinline__ float wave_sum(float v) {
+    v += dpp<kDppXor1>(v);
+    v += dpp<kDppXor2>(v);
+    v += dpp<kDppHalfMirror>(v);
+    v += dpp<kDppMirror>(v);
+    const float a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    const float b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+    const float c = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    const float d = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+    return ((a + b) + c) + d;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp<kDppXor1>(v));
+    v = fmaxf(v, dpp<kDppXor2>(v));
+    v = fmaxf(v, dpp<kDppHalfMirror>(v));
+    v = fmaxf(v, dpp<kDppMirror>(v));
+    const float a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    const float b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+    const float c = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    const float d = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+    return fmaxf(fmaxf(a, b), fmaxf(c, d));
+}
+
+// Block-wide sum for blockDim.x a multiple of 64 (<= 1024); `scratch` holds 16 floats.
+__device__ __forceinline__ float block_sum(float v, float* scratch) {
+    v = wave_sum(v);
+    const int w = threadIdx.x / kWave;
+    const int nw = blockDim.x / kWave;
+    if ((threadIdx.x & (kWave - 1)) == 0) scratch[w] = v;
+    __syncthreads();
+    float t = 0.f;
+    for (int i = 0; i < nw; ++i) t += scratch[i];
+    __syncthreads();
+    return t;
+}
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
+
+__device__ __forceinline__ float half_bits_to_float(uint16_t b) { return static_cast<float>(__builtin_bit_cast(_Float16, b)); }
+// Round-to-nearest-even fp32 -> fp16 bits.
+__device__ __forceinline__ uint16_t float_to_half_bits(float f) { return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f)); }
+
+__device__ __forceinline__ float silu(float g) { return g / (1.f + expf(-g)); }
+
+}  // namespace cllm

@@ -1,0 +1,360 @@
+// Batch-1 weight-streaming matvec for gfx950 (wave64), included by one translation unit per weight
+// type.  Behaviour follows reference src/kernels/matvec_opt.cu:43-157 (y = W x^ with an fp32
+// accumulator, optional fused RMSNorm prologue, STORE / ADD / SWIGLU epilogue, int8 scale per row,
+// int4 fp16 scale per 128 columns); the work decomposition is this file's own:
+//
+//  * A workgroup is 4 waves.  Columns are cut into 2048-wide slices; KS = cols/2048 waves share
+//    one row (one slice each), so the 4 waves of a workgroup cover 4/KS row groups.
+//  * Every lane owns a fixed set of 32 columns of its slice: the 16-byte chunks lane, lane+64, ...
+//    (8 bf16 / 16 int8 / 32 int4 columns per chunk).  Those 32 inputs - normalised when the norm
+//    is fused - are loaded ONCE into VGPRs and reused for every row the wave touches, so the inner
+//    loop reads no LDS at all: only 128-bit non-temporal weight loads, 64 lanes x 16 B = 1 KiB
+//    contiguous per load instruction.
+//  * R rows (rpb) are loaded before any is consumed, for R x (4 KiB bf16 | 2 KiB int8 | 1 KiB int4)
+//    of loads in flight per wave.
+//  * Row sums are wave64 DPP butterflies (deterministic order); with KS > 1 the slice partials
+//    meet in LDS and are added in slice order.  No atomics anywhere.
+//  * The grid is persistent: min(row blocks, CUs x resident workgroups per CU).
+//
+// Widths with cols % 2048 != 0 or cols/2048 not in {1,4} use matvec_generic, which stages x in LDS.
+#pragma once
+
+#include <algorithm>
+
+#include "../kernels.h"
+#include "device.h"
+
+namespace cllm {
+namespace mv {
+
+constexpr int kSlice = 2048;
+constexpr int kThreads = 256;
+
+template <WType WT>
+struct Fmt;
+template <>
+struct Fmt<WType::BF16> {
+    static constexpr int CPC = 8;  // columns per 16-byte chunk
+    static constexpr int CPL = 4;  // chunks per lane per 2048-column slice
+};
+template <>
+struct Fmt<WType::INT8> {
+    static constexpr int CPC = 16;
+    static constexpr int CPL = 2;
+};
+template <>
+struct Fmt<WType::INT4> {
+    static constexpr int CPC = 32;
+    static constexpr int CPL = 1;
+};
+
+template <WType WT>
+__host__ __device__ constexpr size_t row_bytes(int cols) {
+    return static_cast<size_t>(cols) * 16 / Fmt<WT>::CPC;
+}
+
+// Dot of one 16-byte weight chunk with its CPC inputs.  int4 returns sum(u*x) with u = q+8 (the
+// stored nibble); the caller subtracts 8*sum(x).
+template <WType WT>
+__device__ __forceinline__ float chunk_dot(const u32x4 v, const float* x) {
+    float acc = 0.f;
+    if constexpr (WT == WType::BF16) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            acc = fmaf(bf16_lo(v[t]), x[2 * t], acc);
+            acc = fmaf(bf16_hi(v[t]), x[2 * t + 1], acc);
+        }
+    } else if constexpr (WT == WType::INT8) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+                acc = fmaf(static_cast<float>(static_cast<int8_t>(v[t] >> (8 * b))), x[4 * t + b], acc);
+        }
+    } else {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const uint32_t lo = v[t] & 0x0F0F0F0Fu;
+            const uint32_t hi = (v[t] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                acc = fmaf(static_cast<float>((lo >> (8 * b)) & 0xffu), x[8 * t + 2 * b], acc);
+                acc = fmaf(static_cast<float>((hi >> (8 * b)) & 0xffu), x[8 * t + 2 * b + 1], acc);
+            }
+        }
+    }
+    return acc;
+}
+
+template <Epilogue EP>
+__device__ __forceinline__ void store_out(float* y, int r, float d, float du) {
+    if constexpr (EP == Epilogue::STORE) {
+        y[r] = d;
+    } else if constexpr (EP == Epilogue::ADD) {
+        y[r] = y[r] + d;
+    } else {
+        y[r] = silu(d) * du;
+    }
+}
+
+template <WType WT, Epilogue EP, bool NORM, int KS, int R>
+__global__ void __launch_bounds__(kThreads) matvec_fast(MatvecArgs a) {
+    using F = Fmt<WT>;
+    constexpr int NX = F::CPL * F::CPC;  // 32 inputs per lane
+    constexpr int GROUPS = 4 / KS;
+    constexpr int ROWS_WG = GROUPS * R;
+    constexpr bool GLU = EP == Epilogue::SWIGLU;
+    constexpr int NP = GLU ? 2 : 1;
+    __shared__ float scratch[16];
+    __shared__ float part[KS > 1 ? KS * ROWS_WG * NP : 1];
+
+    const int tid = threadIdx.x;
+    const int wave = tid / kWave, lane = tid % kWave;
+    const int slice = wave % KS, grp = wave / KS;
+    const int out_rows = GLU ? a.rows / 2 : a.rows;
+
+    float inv = 1.f;
+    if constexpr (NORM) {
+        float ss = 0.f;
+        for (int j = tid * 4; j < a.cols; j += kThreads * 4) {
+            const f32x4 v = *reinterpret_cast<const f32x4*>(a.x + j);
+            ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+        }
+        ss = block_sum(ss, scratch);
+        inv = rsqrtf(ss / static_cast<float>(a.cols) + a.eps);
+    }
+    float xr[NX];
+    float xsum = 0.f;
+#pragma unroll
+    for (int k = 0; k < F::CPL; ++k) {
+        const int c0 = slice * kSlice + (k * kWave + lane) * F::CPC;
+#pragma unroll
+        for (int j = 0; j < F::CPC; j += 4) {
+            f32x4 v = *reinterpret_cast<const f32x4*>(a.x + c0 + j);
+            if constexpr (NORM) {
+                const f32x4 nw = *reinterpret_cast<const f32x4*>(a.norm_w + c0 + j);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] = v[e] * inv * nw[e];
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                xr[k * F::CPC + j + e] = v[e];
+                xsum += v[e];
+            }
+        }
+    }
+
+    const size_t rb = row_bytes<WT>(a.cols);
+    const char* wl = static_cast<const char*>(a.w) + static_cast<size_t>(slice) * (kSlice * 16 / F::CPC) + lane * 16;
+    const int groups_per_row = a.cols / 128;
+
+    for (int base = blockIdx.x * ROWS_WG; base < out_rows; base += gridDim.x * ROWS_WG) {
+        const int r0 = base + grp * R;
+        u32x4 v[R][F::CPL];
+        u32x4 vu[GLU ? R : 1][F::CPL];
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+            const int r = r0 + i;
+#pragma unroll
+            for (int k = 0; k < F::CPL; ++k) {
+                if (r < out_rows) {
+                    v[i][k] = load_stream(wl + static_cast<size_t>(r) * rb + k * 1024);
+                    if constexpr (GLU) vu[i][k] = load_stream(wl + static_cast<size_t>(r + out_rows) * rb + k * 1024);
+                } else {
+                    v[i][k] = u32x4{0, 0, 0, 0};
+                    if constexpr (GLU) vu[i][k] = u32x4{0, 0, 0, 0};
+                }
+            }
+        }
+        float d[R], du[R];
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+            float s = 0.f, su = 0.f;
+#pragma unroll
+            for (int k = 0; k < F::CPL; ++k) {
+                s += chunk_dot<WT>(v[i][k], xr + k * F::CPC);
+                if constexpr (GLU) su += chunk_dot<WT>(vu[i][k], xr + k * F::CPC);
+            }
+            if constexpr (WT == WType::INT4) {
+                // One 128-column group per lane: lanes 4g..4g+3 share scale g of the slice.
+                const int r = min(r0 + i, out_rows - 1);
+                const uint16_t* sc = static_cast<const uint16_t*>(a.scales);
+                const int gi = slice * (kSlice / 128) + lane / 4;
+                s = half_bits_to_float(sc[static_cast<size_t>(r) * groups_per_row + gi]) * (s - 8.f * xsum);
+                if constexpr (GLU)
+                    su = half_bits_to_float(sc[static_cast<size_t>(r + out_rows) * groups_per_row + gi]) * (su - 8.f * xsum);
+            }
+            d[i] = wave_sum(s);
+            du[i] = GLU ? wave_sum(su) : 0.f;
+        }
+
+        // Lane i (< R) holds row r0 + i.
+        float mine = d[0], mine_u = du[0];
+#pragma unroll
+        for (int i = 1; i < R; ++i) {
+            if (lane == i) {
+                mine = d[i];
+                mine_u = du[i];
+            }
+        }
+        if constexpr (KS == 1) {
+            const int r = r0 + lane;
+            if (lane < R && r < out_rows) {
+                if constexpr (WT == WType::INT8) {
+                    const float* sc = static_cast<const float*>(a.scales);
+                    mine *= sc[r];
+                    if constexpr (GLU) mine_u *= sc[r + out_rows];
+                }
+                store_out<EP>(a.y, r, mine, mine_u);
+            }
+        } else {
+            if (lane < R) {
+                const int slot = (slice * ROWS_WG + grp * R + lane) * NP;
+                part[slot] = mine;
+                if constexpr (GLU) part[slot + 1] = mine_u;
+            }
+            __syncthreads();
+            if (tid < ROWS_WG && base + tid < out_rows) {
+                const int r = base + tid;
+                float s = 0.f, su = 0.f;
+#pragma unroll
+                for (int q = 0; q < KS; ++q) {
+                    s += part[(q * ROWS_WG + tid) * NP];
+                    if constexpr (GLU) su += part[(q * ROWS_WG + tid) * NP + 1];
+                }
+                if constexpr (WT == WType::INT8) {
+                    const float* sc = static_cast<const float*>(a.scales);
+                    s *= sc[r];
+                    if constexpr (GLU) su *= sc[r + out_rows];
+                }
+                store_out<EP>(a.y, r, s, su);
+            }
+            __syncthreads();
+        }
+    }
+}
+
+// Any cols that is a multiple of 1024 (up to 12288): x^ staged in LDS, one wave per row.
+template <WType WT, Epilogue EP, bool NORM>
+__global__ void __launch_bounds__(kThreads) matvec_generic(MatvecArgs a) {
+    using F = Fmt<WT>;
+    extern __shared__ float xs[];
+    __shared__ float scratch[16];
+    constexpr bool GLU = EP == Epilogue::SWIGLU;
+    const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+    const int out_rows = GLU ? a.rows / 2 : a.rows;
+    float inv = 1.f;
+    if constexpr (NORM) {
+        float ss = 0.f;
+        for (int j = tid; j < a.cols; j += kThreads) ss += a.x[j] * a.x[j];
+        ss = block_sum(ss, scratch);
+        inv = rsqrtf(ss / static_cast<float>(a.cols) + a.eps);
+    }
+    for (int j = tid; j < a.cols; j += kThreads) xs[j] = NORM ? a.x[j] * inv * a.norm_w[j] : a.x[j];
+    __syncthreads();
+
+    const size_t rb = row_bytes<WT>(a.cols);
+    const int nchunk = a.cols / F::CPC;
+    const int groups_per_row = a.cols / 128;
+    for (int r = blockIdx.x * 4 + wave; r < out_rows; r += gridDim.x * 4) {
+        float s = 0.f, su = 0.f;
+        for (int c = lane; c < nchunk; c += kWave) {
+            const float* x = xs + c * F::CPC;
+            const char* p = static_cast<const char*>(a.w) + static_cast<size_t>(r) * rb + c * 16;
+            float t = chunk_dot<WT>(load_stream(p), x);
+            float tu = GLU ? chunk_dot<WT>(load_stream(p + static_cast<size_t>(out_rows) * rb), x) : 0.f;
+            if constexpr (WT == WType::INT4) {
+                float xsum = 0.f;
+#pragma unroll
+                for (int j = 0; j < F::CPC; ++j) xsum += x[j];
+                const uint16_t* sc = static_cast<const uint16_t*>(a.scales);
+                const int gi = c * F::CPC / 128;
+                t = half_bits_to_float(sc[static_cast<size_t>(r) * groups_per_row + gi]) * (t - 8.f * xsum);
+                if constexpr (GLU)
+                    tu = half_bits_to_float(sc[static_cast<size_t>(r + out_rows) * groups_per_row + gi]) * (tu - 8.f * xsum);
+            }
+            s += t;
+            su += tu;
+        }
+        s = wave_sum(s);
+        su = GLU ? wave_sum(su) : 0.f;
+        if (lane == 0) {
+            if constexpr (WT == WType::INT8) {
+                const float* sc = static_cast<const float*>(a.scales);
+                s *= sc[r];
+                if constexpr (GLU) su *= sc[r + out_rows];
+            }
+            store_out<EP>(a.y, r, s, su);
+        }
+    }
+}
+
+template <typename K>
+int resident_blocks(K kernel, size_t smem) {
+    int b = 0;
+    CLLM_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, kernel, kThreads, smem));
+    CLLM_INTERNAL(b > 0, "matvec kernel cannot be resident");
+    return b;
+}
+
+template <WType WT, Epilogue EP, bool NORM, int KS, int R>
+void launch_fast(const MatvecArgs& a, hipStream_t s) {
+    auto k = matvec_fast<WT, EP, NORM, KS, R>;
+    static const int occ = resident_blocks(k, 0);
+    const int out_rows = EP == Epilogue::SWIGLU ? a.rows / 2 : a.rows;
+    constexpr int ROWS_WG = (4 / KS) * R;
+    const int need = (out_rows + ROWS_WG - 1) / ROWS_WG;
+    const int grid = std::min(need, device_cu_count() * occ);
+    hipLaunchKernelGGL(k, dim3(grid), dim3(kThreads), 0, s, a);
+    CLLM_HIP(hipGetLastError());
+}
+
+template <WType WT, Epilogue EP, bool NORM>
+void launch_generic(const MatvecArgs& a, hipStream_t s) {
+    auto k = matvec_generic<WT, EP, NORM>;
+    const size_t smem = static_cast<size_t>(a.cols) * sizeof(float);
+    const int occ = resident_blocks(k, smem);
+    const int out_rows = EP == Epilogue::SWIGLU ? a.rows / 2 : a.rows;
+    const int grid = std::min((out_rows + 3) / 4, device_cu_count() * occ);
+    hipLaunchKernelGGL(k, dim3(grid), dim3(kThreads), smem, s, a);
+    CLLM_HIP(hipGetLastError());
+}
+
+template <WType WT, Epilogue EP, bool NORM, int KS>
+void pick_r(int rpb, const MatvecArgs& a, hipStream_t s) {
+    switch (rpb) {
+        case 1: return launch_fast<WT, EP, NORM, KS, 1>(a, s);
+        case 2: return launch_fast<WT, EP, NORM, KS, 2>(a, s);
+        case 4: return launch_fast<WT, EP, NORM, KS, 4>(a, s);
+        case 8: return launch_fast<WT, EP, NORM, KS, 8>(a, s);
+    }
+    throw ArgError("matvec: rpb must be 1, 2, 4 or 8");
+}
+
+template <WType WT, Epilogue EP, bool NORM>
+void pick_shape(int rpb, const MatvecArgs& a, hipStream_t s) {
+    if (a.cols == 2048) return pick_r<WT, EP, NORM, 1>(rpb, a, s);
+    if (a.cols == 8192) return pick_r<WT, EP, NORM, 4>(rpb, a, s);
+    return launch_generic<WT, EP, NORM>(a, s);
+}
+
+template <WType WT>
+void launch_wt(Epilogue ep, const MatvecArgs& a, int rpb, hipStream_t s) {
+    const bool norm = a.norm_w != nullptr;
+    switch (ep) {
+        case Epilogue::STORE:
+            return norm ? pick_shape<WT, Epilogue::STORE, true>(rpb, a, s) : pick_shape<WT, Epilogue::STORE, false>(rpb, a, s);
+        case Epilogue::ADD:
+            return norm ? pick_shape<WT, Epilogue::ADD, true>(rpb, a, s) : pick_shape<WT, Epilogue::ADD, false>(rpb, a, s);
+        case Epilogue::SWIGLU:
+            return norm ? pick_shape<WT, Epilogue::SWIGLU, true>(rpb, a, s) : pick_shape<WT, Epilogue::SWIGLU, false>(rpb, a, s);
+    }
+    throw ArgError("matvec: bad epilogue");
+}
+
+}  // namespace mv
+
+template <WType WT>
+void launch_matvec_wt(Epilogue ep, const MatvecArgs& a, int rpb, hipStream_t s);
+
+}  // namespace cllm

@@ -1,0 +1,49 @@
+"""Shared fixtures.
+
+Tests marked ``gpu`` run the HIP path through the C ABI and compare it with ``oracle`` (the CPU
+restatement of the reference).  Unmarked tests run on the CPU only: the oracle against the
+reference's known answers and golden vectors, the file format, and the ABI's host-side behaviour.
+"""
+import os
+import sys
+from pathlib import Path
+
+import pytest
+
+REPO = Path(__file__).resolve().parents[1]
+if str(REPO) not in sys.path:
+    sys.path.insert(0, str(REPO))
+
+# The box gives one GPU process a share of 16 cores; do not oversubscribe the CPU oracle.
+os.environ.setdefault("OMP_NUM_THREADS", "16")
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU")
+
+
+@pytest.fixture(scope="session")
+def lib():
+    """The built libcudallm.so.  A missing build is an error, never a skip or a fallback."""
+    from cudallm_amd import engine as E
+    return E.lib()
+
+
+@pytest.fixture(scope="session")
+def gpu(lib):
+    """Fails loudly when a gpu test runs without a visible GPU."""
+    import torch
+    if not torch.cuda.is_available():
+        pytest.fail("gpu test without a visible GPU")
+    name = torch.cuda.get_device_properties(0).gcnArchName
+    print(f"[gpu] device 0: {torch.cuda.get_device_name(0)} ({name})", flush=True)
+    return name
+
+
+@pytest.fixture(scope="session")
+def model_dir(tmp_path_factory):
+    d = os.environ.get("CUDALLM_TEST_MODELS")
+    if d:
+        Path(d).mkdir(parents=True, exist_ok=True)
+        return Path(d)
+    return tmp_path_factory.mktemp("models")

@@ -1,0 +1,212 @@
+"""GPU parity of the whole decode step: engine (through the C ABI) vs the CPU oracle.
+
+Follows the reference's tests/test_engine_vs_reference.py:10-94 (same option configurations and
+tolerances: residual rel-L2 < 1e-3, logits max |d| < 2e-2, argmax agreement, next == argmax,
+bit-identical re-run after reset) on seeded synthetic Llama-3.2-1B-shaped files
+instead of the HF checkpoint, plus graph-vs-eager identity, greedy decoding and state errors.
+"""
+import os
+
+import numpy as np
+import pytest
+
+from cudallm_amd import engine as E
+from cudallm_amd import synth
+from oracle.model import OracleModel
+
+pytestmark = [pytest.mark.gpu, pytest.mark.timeout(900)]
+
+N_TOK = 16
+TOKENS = [128000] + [int(t) for t in np.random.default_rng(2024).integers(0, 128256, N_TOK - 1)]
+WEIGHT_BYTES = {"bf16": 2471764096, "int8": 1238037632, "int4": 637452416}
+
+# (dtype, matvec, attn, fuse, graph): reference tests/test_engine_vs_reference.py:11-22
+CONFIGS = [("bf16", "naive", "naive", 0, 0), ("bf16", "opt", "naive", 0, 0), ("bf16", "opt", "opt", 0, 0),
+           ("bf16", "opt", "opt", 1, 0), ("bf16", "opt", "opt", 0, 1), ("bf16", "opt", "opt", 1, 1),
+           ("int8", "opt", "opt", 1, 1), ("int8", "opt", "opt", 1, 0), ("int4", "opt", "opt", 1, 1),
+           ("int4", "opt", "opt", 1, 0)]
+
+
+def _id(c):
+    return "-".join(str(v) for v in c)
+
+
+def _threads() -> int:
+    return min(16, os.cpu_count() or 1)
+
+
+@pytest.fixture(scope="module")
+def model_path(gpu, model_dir):
+    cache = {}
+
+    def get(wd):
+        if wd not in cache:
+            p = model_dir / f"synth_seed1234_{wd}.cudallm"
+            if not p.exists():
+                print(f"[engine] writing {p}", flush=True)
+                synth.write_model(p, wd, seed=1234)
+            cache[wd] = p
+        return cache[wd]
+    return get
+
+
+@pytest.fixture(scope="module")
+def oracle_out(model_path):
+    cache = {}
+
+    def get(wd):
+        if wd not in cache:
+            print(f"[engine] oracle {wd}", flush=True)
+            m = OracleModel(model_path(wd), cache_dense=True, threads=_threads())
+            logits, res = [], []
+            for t in TOKENS:
+                lg, r = m.step(t)
+                logits.append(lg.numpy())
+                res.append(np.stack([v.numpy() for v in r]))
+            cache[wd] = (np.stack(logits), np.stack(res))
+            del m
+        return cache[wd]
+    return get
+
+
+def _run(eng, ids, graph):
+    logits, res, nexts = [], [], []
+    for t in ids:
+        if graph:
+            nxt, lg = eng.step(t, want_logits=True)
+            r = None
+        else:
+            nxt, lg, r = eng.step_debug(t)
+        logits.append(lg)
+        res.append(r)
+        nexts.append(nxt)
+    return np.stack(logits), (None if graph else np.stack(res)), nexts
+
+
+@pytest.fixture(scope="module")
+def engine_runs(model_path):
+    cache = {}
+
+    def get(cfg):
+        if cfg not in cache:
+            wd, mv, at, fuse, graph = cfg
+            print(f"[engine] run {_id(cfg)}", flush=True)
+            with E.Engine(model_path(wd), matvec=mv, attn=at, fuse=bool(fuse), cuda_graph=bool(graph)) as eng:
+                logits, res, nexts = _run(eng, TOKENS, graph)
+                eng.reset()
+                rerun, _, _ = _run(eng, TOKENS[:4], graph)
+                assert eng.pos == 4
+            cache[cfg] = dict(logits=logits, res=res, nexts=nexts, rerun=rerun)
+        return cache[cfg]
+    return get
+
+
+@pytest.mark.parametrize("cfg", [c for c in CONFIGS if not c[4]], ids=_id)
+def test_residuals(cfg, engine_runs, oracle_out):
+    run = engine_runs(cfg)
+    _, ref = oracle_out(cfg[0])
+    assert run["res"].shape == ref.shape
+    for p in range(ref.shape[0]):
+        for k in range(ref.shape[1]):
+            a, b = run["res"][p, k].astype(np.float64), ref[p, k].astype(np.float64)
+            rel = np.linalg.norm(a - b) / np.linalg.norm(b)
+            assert rel < 1e-3, f"position {p}, residual {k}: relative error {rel:.3e}"
+
+
+@pytest.mark.parametrize("cfg", CONFIGS, ids=_id)
+def test_logits(cfg, engine_runs, oracle_out):
+    run = engine_runs(cfg)
+    ref, _ = oracle_out(cfg[0])
+    diff = np.max(np.abs(run["logits"] - ref))
+    assert diff < 2e-2, f"max |engine - oracle| logit difference {diff:.3e}"
+    agree = int(np.sum(np.argmax(run["logits"], axis=1) == np.argmax(ref, axis=1)))
+    assert agree >= N_TOK - 1, f"argmax agrees at {agree}/{N_TOK} positions"
+
+
+@pytest.mark.parametrize("cfg", CONFIGS, ids=_id)
+def test_next_token_is_argmax(cfg, engine_runs):
+    run = engine_runs(cfg)
+    assert run["nexts"] == [int(np.argmax(lg)) for lg in run["logits"]]
+
+
+@pytest.mark.parametrize("cfg", CONFIGS, ids=_id)
+def test_reset_determinism(cfg, engine_runs):
+    run = engine_runs(cfg)
+    np.testing.assert_array_equal(run["rerun"], run["logits"][:4])
+
+
+@pytest.mark.parametrize("wd", ["bf16", "int8", "int4"])
+def test_graph_replay_equals_eager(wd, engine_runs):
+    np.testing.assert_array_equal(engine_runs((wd, "opt", "opt", 1, 1))["logits"],
+                                  engine_runs((wd, "opt", "opt", 1, 0))["logits"])
+
+
+@pytest.mark.parametrize("wd", ["bf16", "int8", "int4"])
+def test_greedy_matches_oracle(wd, model_path):
+    """Greedy decoding (token -1 reuses the device argmax) against the oracle teacher-forced on the
+    engine's own tokens.  A differing token is accepted only at a near-tie of the oracle's top two
+    logits (closer than the 2e-2 logits tolerance); the margin of each such case is printed."""
+    prompt, n_new = TOKENS[:6], 24
+    with E.Engine(model_path(wd)) as eng:
+        for t in prompt[:-1]:
+            eng.step_async(t)
+        nxt, _ = eng.step(prompt[-1])
+        gen = [nxt]
+        for _ in range(n_new - 1):
+            nxt, _ = eng.step(None)
+            gen.append(nxt)
+        # The same sequence fully pipelined (no host sync until the last step) ends on the same token.
+        eng.reset()
+        for t in prompt:
+            eng.step_async(t)
+        for _ in range(n_new - 2):
+            eng.step_async(None)
+        last, _ = eng.step(None)
+        assert last == gen[-1] and eng.pos == len(prompt) + n_new - 1
+    m = OracleModel(model_path(wd), cache_dense=True, threads=_threads())
+    lg = None
+    for t in prompt:
+        lg, _ = m.step(t)
+    mism = []
+    for i, tok in enumerate(gen):
+        ref = lg.numpy()
+        best = int(np.argmax(ref))
+        if best != tok:
+            margin = float(ref[best] - ref[tok])
+            mism.append((i, tok, best, margin))
+            assert margin < 2e-2, f"step {i}: engine {tok}, oracle {best}, margin {margin:.3e}"
+        if i + 1 < len(gen):
+            lg, _ = m.step(tok)
+    print(f"[greedy {wd}] {len(gen)} tokens, {len(mism)} near-tie differences {mism}")
+
+
+def test_config_and_weight_bytes(model_path):
+    for wd in ("bf16", "int8", "int4"):
+        with E.Engine(model_path(wd), max_seq_len=256) as eng:
+            c = eng.config
+            assert c["weight_bytes"] == WEIGHT_BYTES[wd]
+            assert (c["hidden"], c["inter"], c["n_layers"], c["n_heads"], c["n_kv_heads"], c["head_dim"], c["vocab"]) \
+                == (2048, 8192, 16, 32, 8, 64, 128256)
+            assert c["max_seq_len"] == 256 and c["group_size"] == (128 if wd == "int4" else 0)
+            assert abs(c["rms_eps"] - 1e-5) < 1e-12
+
+
+def test_sequence_full_and_token_range(model_path):
+    with E.Engine(model_path("int4"), max_seq_len=128) as eng:
+        with pytest.raises(E.CudaLLMError) as ei:
+            eng.step(128256)
+        assert ei.value.code == 1
+        with pytest.raises(E.CudaLLMError) as ei:
+            eng.step(-2)
+        assert ei.value.code == 1
+        eng.step_async(1)
+        for _ in range(127):
+            eng.step_async(None)
+        assert eng.pos == 128
+        with pytest.raises(E.CudaLLMError) as ei:
+            eng.step(None)
+        assert ei.value.code == 5 and "full" in str(ei.value)
+        eng.reset()
+        assert eng.pos == 0
+        nxt, lg = eng.step(5, want_logits=True)
+        assert eng.pos == 1 and nxt == int(np.argmax(lg))
