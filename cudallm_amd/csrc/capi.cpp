@@ -191,6 +191,15 @@ int cudallm_step_debug(cudallm_engine* e, int token, float* residuals_out, float
     });
 }
 
+int cudallm_step_profile(cudallm_engine* e, int token, unsigned long long* stamps_out, long long capacity,
+                         int* grid_out) {
+    return guarded([&] {
+        CLLM_REQUIRE(e && e->impl && grid_out, "cudallm_step_profile: null argument");
+        CLLM_REQUIRE(token >= -1, "cudallm_step_profile: token must be >= -1");
+        *grid_out = e->impl->step_profile(token, stamps_out, static_cast<long>(capacity));
+    });
+}
+
 int cudallm_kernel_matvec(int impl, int weight_dtype, int epilogue, int fuse_norm, int rpb, const void* w,
                           unsigned long long w_bytes, const void* scales, unsigned long long scales_bytes,
                           const float* x, const float* norm_w, float eps, float* y, int rows, int cols) {

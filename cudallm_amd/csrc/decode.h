@@ -1,0 +1,68 @@
+// Parameters of the persistent decode-step kernel (shared by host and device code).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "common.h"
+
+namespace cllm {
+
+// Per-layer weight pointers, kept in device memory.
+struct DecodeLayer {
+    const float* attn_norm;
+    const void* wqkv;
+    const void* sqkv;
+    const void* wo;
+    const void* so;
+    const float* ffn_norm;
+    const void* wgu;
+    const void* sgu;
+    const void* wd;
+    const void* sd;
+};
+
+// Tagged vectors: every element is a 64-bit word (fp32 value in the low half, the epoch tag of
+// the phase that produced it in the high half), written and read with relaxed agent-scope 64-bit
+// atomics.  A reader waits for the tag of the current phase, so one read both synchronises with
+// the producing workgroup and delivers the value.
+struct DecodeParams {
+    const DecodeLayer* layers;
+    const void* emb;
+    const void* emb_s;
+    const float* inv_freq;
+    const float* final_norm;
+    uint16_t* k_cache;  // fp16 [layer][kv_head][max_seq][head_dim]
+    uint16_t* v_cache;
+    int max_seq;
+    uint64_t* tx;    // [n_layers + 1][hidden]  residual stream at each layer input (index l+1 = after layer l)
+    uint64_t* txa;   // [n_layers][hidden]      residual after the attention block
+    uint64_t* tqkv;  // [n_layers][3072]        q|k (rotated) | v
+    uint64_t* tatt;  // [n_layers][2048]        attention output
+    uint64_t* tpart; // [n_layers][32][max_seq/128][66]  split partials: o[64], m, l
+    uint64_t* tact;  // [n_layers][inter]       SwiGLU output
+    uint64_t* targ;  // [grid][2]               per-workgroup argmax (value, index)
+    float* logits;
+    int* d_token;
+    int* d_pos;
+    unsigned* d_step;  // launch counter: epoch base of the tags, never reset
+    unsigned* d_err;   // sticky: set when a wait exceeded its bound
+    float* residuals;  // optional [(n_layers + 1) * hidden] snapshots (step_debug)
+    unsigned long long* stamps;  // optional [grid][kStampSlots] phase-end timestamps (100 MHz clock)
+    float eps;
+};
+
+// Timestamp slots per workgroup: 0 = start, 1 + 6 l + k = end of phase k of layer l
+// (k: 0 qkv, 1 attention, 2 split merge, 3 wo, 4 gate_up, 5 down), 97 = lm_head end,
+// 98 = final argmax end (workgroup 0 only).
+constexpr int kStampSlots = 128;
+
+constexpr int kDecodeThreads = 256;
+
+// Enqueue one decode step (one launch).  `grid` workgroups must all be co-resident.
+void launch_decode(WType wt, const DecodeParams& p, int grid, hipStream_t s);
+// Workgroups of the decode kernel that fit on the device at once for this weight type.
+int decode_max_grid(WType wt);
+
+}  // namespace cllm

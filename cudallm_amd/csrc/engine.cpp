@@ -9,6 +9,9 @@
 #include "engine.h"
 
 #include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <vector>
 
 namespace cllm {
 
@@ -61,6 +64,21 @@ Engine::Engine(const std::string& path, const EngineOptions& opts) : opts_(opts)
                      o_pml = cv.take<float>(NH * NS * 2), o_av = cv.take<float>(kArgmaxParts),
                      o_ai = cv.take<int>(kArgmaxParts), o_tok = cv.take<int>(1), o_pos = cv.take<int>(1),
                      o_k = cv.take<uint16_t>(L * KV * S * D), o_v = cv.take<uint16_t>(L * KV * S * D);
+        // Persistent decode kernel: fused + opt options, contexts up to 8192 (one split per lane
+        // in the LSE merge), and one co-resident workgroup per CU.  CUDALLM_PERSISTENT=0 selects
+        // the kernel-per-op graph instead (for comparisons).
+        const char* env = std::getenv("CUDALLM_PERSISTENT");
+        const bool want = opts_.fuse && opts_.matvec == 1 && opts_.attn == 1 && S <= 8192 && !(env && !std::strcmp(env, "0"));
+        grid_ = device_cu_count();
+        persistent_ = want && grid_ <= 4096 && decode_max_grid(c.wt) >= grid_;
+        const size_t QKV = (NH + 2 * KV) * D;
+        const size_t o_tx = cv.take<uint64_t>((L + 1) * H), o_txa = cv.take<uint64_t>(L * H),
+                     o_tqkv = cv.take<uint64_t>(L * QKV), o_tatt = cv.take<uint64_t>(L * NH * D),
+                     o_tpart = cv.take<uint64_t>(persistent_ ? L * NH * NS * (D + 2) : 1),
+                     o_tact = cv.take<uint64_t>(L * I), o_targ = cv.take<uint64_t>(2 * 4096),
+                     o_res = cv.take<float>((L + 1) * H), o_layers = cv.take<DecodeLayer>(L),
+                     o_step = cv.take<unsigned>(1), o_err = cv.take<unsigned>(1),
+                     o_stamps = cv.take<unsigned long long>(static_cast<size_t>(grid_) * kStampSlots);
         CLLM_HIP(hipMalloc(&arena_, cv.off));
         CLLM_HIP(hipMemset(arena_, 0, cv.off));
         char* b = static_cast<char*>(arena_);
@@ -80,6 +98,43 @@ Engine::Engine(const std::string& path, const EngineOptions& opts) : opts_(opts)
         d_pos_ = reinterpret_cast<int*>(b + o_pos);
         k_cache_ = reinterpret_cast<uint16_t*>(b + o_k);
         v_cache_ = reinterpret_cast<uint16_t*>(b + o_v);
+        d_res_ = reinterpret_cast<float*>(b + o_res);
+        d_err_ = reinterpret_cast<unsigned*>(b + o_err);
+        d_stamps_ = reinterpret_cast<unsigned long long*>(b + o_stamps);
+        const Weights& W = *weights_;
+        std::vector<DecodeLayer> table(L);
+        for (size_t l = 0; l < L; ++l) {
+            const LayerWeights& lw = W.layers[l];
+            table[l] = {lw.attn_norm, lw.wqkv.w, lw.wqkv.scales, lw.wo.w, lw.wo.scales,
+                        lw.ffn_norm, lw.w_gate_up.w, lw.w_gate_up.scales, lw.w_down.w, lw.w_down.scales};
+        }
+        auto* d_layers = reinterpret_cast<DecodeLayer*>(b + o_layers);
+        CLLM_HIP(hipMemcpy(d_layers, table.data(), sizeof(DecodeLayer) * L, hipMemcpyHostToDevice));
+        const unsigned one = 1;  // tags of step 0 would equal the zero-filled buffers
+        CLLM_HIP(hipMemcpy(b + o_step, &one, sizeof(one), hipMemcpyHostToDevice));
+        dp_.layers = d_layers;
+        dp_.emb = W.tok_embeddings.w;
+        dp_.emb_s = W.tok_embeddings.scales;
+        dp_.inv_freq = W.inv_freq;
+        dp_.final_norm = W.final_norm;
+        dp_.k_cache = k_cache_;
+        dp_.v_cache = v_cache_;
+        dp_.max_seq = max_seq_;
+        dp_.tx = reinterpret_cast<uint64_t*>(b + o_tx);
+        dp_.txa = reinterpret_cast<uint64_t*>(b + o_txa);
+        dp_.tqkv = reinterpret_cast<uint64_t*>(b + o_tqkv);
+        dp_.tatt = reinterpret_cast<uint64_t*>(b + o_tatt);
+        dp_.tpart = reinterpret_cast<uint64_t*>(b + o_tpart);
+        dp_.tact = reinterpret_cast<uint64_t*>(b + o_tact);
+        dp_.targ = reinterpret_cast<uint64_t*>(b + o_targ);
+        dp_.logits = logits_;
+        dp_.d_token = d_token_;
+        dp_.d_pos = d_pos_;
+        dp_.d_step = reinterpret_cast<unsigned*>(b + o_step);
+        dp_.d_err = d_err_;
+        dp_.residuals = nullptr;
+        dp_.stamps = nullptr;
+        dp_.eps = c.rms_eps;
         CLLM_HIP(hipDeviceSynchronize());
     } catch (...) {
         release();
@@ -106,8 +161,19 @@ Engine::~Engine() {
     release();
 }
 
+void Engine::check_device_error() {
+    unsigned e = 0;
+    CLLM_HIP(hipMemcpy(&e, d_err_, sizeof(e), hipMemcpyDeviceToHost));
+    if (e) {
+        throw DeviceError(
+            "persistent decode kernel: a cross-workgroup wait exceeded its bound (were all workgroups "
+            "co-resident? another process may be sharing the GPU); the results of this sequence are invalid");
+    }
+}
+
 void Engine::reset() {
     CLLM_HIP(hipStreamSynchronize(stream_));
+    if (persistent_) check_device_error();
     launch_set_token(d_pos_, 0, stream_);  // a kernel, not a memset
     CLLM_HIP(hipStreamSynchronize(stream_));
     host_pos_ = 0;
@@ -121,7 +187,10 @@ void Engine::step(int token, float* logits_out, int* next_token_out) {
         if (!exec_) {
             CLLM_HIP(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
             try {
-                enqueue_forward(nullptr);
+                if (persistent_)
+                    launch_decode(config().wt, dp_, grid_, stream_);
+                else
+                    enqueue_forward(nullptr);
             } catch (...) {
                 hipGraph_t broken = nullptr;
                 (void)hipStreamEndCapture(stream_, &broken);
@@ -132,12 +201,15 @@ void Engine::step(int token, float* logits_out, int* next_token_out) {
             CLLM_HIP(hipGraphInstantiate(&exec_, graph_, nullptr, nullptr, 0));
         }
         CLLM_HIP(hipGraphLaunch(exec_, stream_));
+    } else if (persistent_) {
+        launch_decode(config().wt, dp_, grid_, stream_);
     } else {
         enqueue_forward(nullptr);
     }
     host_pos_ += 1;
     if (logits_out || next_token_out) {
         CLLM_HIP(hipStreamSynchronize(stream_));
+        if (persistent_) check_device_error();
         if (logits_out)
             CLLM_HIP(hipMemcpy(logits_out, logits_, sizeof(float) * config().vocab, hipMemcpyDeviceToHost));
         if (next_token_out) CLLM_HIP(hipMemcpy(next_token_out, d_token_, sizeof(int), hipMemcpyDeviceToHost));
@@ -149,11 +221,40 @@ void Engine::step_debug(int token, float* residuals_out, float* logits_out, int*
     CLLM_REQUIRE(token >= -1 && token < config().vocab, "step_debug: token out of range");
     CLLM_REQUIRE(residuals_out, "step_debug: residuals_out is null");
     if (token >= 0) launch_set_token(d_token_, token, stream_);
-    enqueue_forward(residuals_out);
+    if (persistent_) {
+        DecodeParams p = dp_;
+        p.residuals = d_res_;
+        launch_decode(config().wt, p, grid_, stream_);
+    } else {
+        enqueue_forward(residuals_out);
+    }
     host_pos_ += 1;
     CLLM_HIP(hipStreamSynchronize(stream_));
+    if (persistent_) {
+        check_device_error();
+        const ModelConfig& c = config();
+        CLLM_HIP(hipMemcpy(residuals_out, d_res_, sizeof(float) * (c.n_layers + 1) * c.hidden, hipMemcpyDeviceToHost));
+    }
     if (logits_out) CLLM_HIP(hipMemcpy(logits_out, logits_, sizeof(float) * config().vocab, hipMemcpyDeviceToHost));
     if (next_token_out) CLLM_HIP(hipMemcpy(next_token_out, d_token_, sizeof(int), hipMemcpyDeviceToHost));
+}
+
+int Engine::step_profile(int token, unsigned long long* stamps_out, long capacity) {
+    if (!persistent_) throw StateError("step_profile: this engine does not use the persistent decode kernel");
+    if (host_pos_ >= max_seq_) throw StateError("step_profile: the sequence is full (pos == max_seq_len); call reset()");
+    CLLM_REQUIRE(token >= -1 && token < config().vocab, "step_profile: token out of range");
+    CLLM_REQUIRE(stamps_out && capacity >= static_cast<long>(grid_) * kStampSlots,
+                 "step_profile: stamps_out must hold grid * 128 values");
+    if (token >= 0) launch_set_token(d_token_, token, stream_);
+    CLLM_HIP(hipMemsetAsync(d_stamps_, 0, sizeof(unsigned long long) * grid_ * kStampSlots, stream_));
+    DecodeParams p = dp_;
+    p.stamps = d_stamps_;
+    launch_decode(config().wt, p, grid_, stream_);
+    host_pos_ += 1;
+    CLLM_HIP(hipStreamSynchronize(stream_));
+    check_device_error();
+    CLLM_HIP(hipMemcpy(stamps_out, d_stamps_, sizeof(unsigned long long) * grid_ * kStampSlots, hipMemcpyDeviceToHost));
+    return grid_;
 }
 
 void Engine::linear(const Linear& L, const float* x, float* y, Epilogue ep, const float* norm_w) {

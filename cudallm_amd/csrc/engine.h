@@ -6,6 +6,7 @@
 #include <memory>
 #include <string>
 
+#include "decode.h"
 #include "kernels.h"
 #include "weights.h"
 
@@ -39,10 +40,13 @@ public:
     void reset();
     void step(int token, float* logits_out, int* next_token_out);
     void step_debug(int token, float* residuals_out, float* logits_out, int* next_token_out);
+    // One step of the persistent kernel with per-phase timestamps; returns the grid size.
+    int step_profile(int token, unsigned long long* stamps_out, long capacity);
 
 private:
     void enqueue_forward(float* residuals_out);
     void linear(const Linear& L, const float* x, float* y, Epilogue ep, const float* norm_w);
+    void check_device_error();
     void release() noexcept;
 
     std::unique_ptr<Weights> weights_;
@@ -59,6 +63,14 @@ private:
           *act_ = nullptr, *logits_ = nullptr, *part_o_ = nullptr, *part_ml_ = nullptr, *arg_v_ = nullptr;
     int *arg_i_ = nullptr, *d_token_ = nullptr, *d_pos_ = nullptr;
     uint16_t *k_cache_ = nullptr, *v_cache_ = nullptr;  // fp16 [layer][kv_head][max_seq][head_dim]
+
+    // Persistent decode kernel (fused + opt options): one launch per token.
+    bool persistent_ = false;
+    int grid_ = 0;
+    DecodeParams dp_{};
+    float* d_res_ = nullptr;  // residual snapshots for step_debug
+    unsigned* d_err_ = nullptr;
+    unsigned long long* d_stamps_ = nullptr;
 };
 
 }  // namespace cllm

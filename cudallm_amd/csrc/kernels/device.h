@@ -15,8 +15,17 @@ constexpr int kWave = 64;
 
 // 128-bit load marked non-temporal: weights are read exactly once per decode step, so they
 // should not displace the activations and the KV cache from the caches.
+// The pointer is cast to the global address space so the load is a global_load even when the
+// pointer itself was read from memory (a generic pointer would become a slower flat_load).
+typedef const __attribute__((address_space(1))) u32x4 global_u32x4;
 __device__ __forceinline__ u32x4 load_stream(const void* p) {
-    return __builtin_nontemporal_load(static_cast<const u32x4*>(p));
+    return __builtin_nontemporal_load((global_u32x4*)p);
+}
+
+// Plain load through the global address space (for pointers that were read from memory).
+template <typename T>
+__device__ __forceinline__ T gload(const T* p) {
+    return *((const __attribute__((address_space(1))) T*)p);
 }
 
 // DPP move of a float within 16-lane rows (control words of the gfx9 DPP encoding).

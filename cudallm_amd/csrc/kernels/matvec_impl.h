@@ -23,68 +23,13 @@
 
 #include "../kernels.h"
 #include "device.h"
+#include "dot.h"
 
 namespace cllm {
 namespace mv {
 
 constexpr int kSlice = 2048;
 constexpr int kThreads = 256;
-
-template <WType WT>
-struct Fmt;
-template <>
-struct Fmt<WType::BF16> {
-    static constexpr int CPC = 8;  // columns per 16-byte chunk
-    static constexpr int CPL = 4;  // chunks per lane per 2048-column slice
-};
-template <>
-struct Fmt<WType::INT8> {
-    static constexpr int CPC = 16;
-    static constexpr int CPL = 2;
-};
-template <>
-struct Fmt<WType::INT4> {
-    static constexpr int CPC = 32;
-    static constexpr int CPL = 1;
-};
-
-template <WType WT>
-__host__ __device__ constexpr size_t row_bytes(int cols) {
-    return static_cast<size_t>(cols) * 16 / Fmt<WT>::CPC;
-}
-
-// Dot of one 16-byte weight chunk with its CPC inputs.  int4 returns sum(u*x) with u = q+8 (the
-// stored nibble); the caller subtracts 8*sum(x).
-template <WType WT>
-__device__ __forceinline__ float chunk_dot(const u32x4 v, const float* x) {
-    float acc = 0.f;
-    if constexpr (WT == WType::BF16) {
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            acc = fmaf(bf16_lo(v[t]), x[2 * t], acc);
-            acc = fmaf(bf16_hi(v[t]), x[2 * t + 1], acc);
-        }
-    } else if constexpr (WT == WType::INT8) {
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-#pragma unroll
-            for (int b = 0; b < 4; ++b)
-                acc = fmaf(static_cast<float>(static_cast<int8_t>(v[t] >> (8 * b))), x[4 * t + b], acc);
-        }
-    } else {
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const uint32_t lo = v[t] & 0x0F0F0F0Fu;
-            const uint32_t hi = (v[t] >> 4) & 0x0F0F0F0Fu;
-#pragma unroll
-            for (int b = 0; b < 4; ++b) {
-                acc = fmaf(static_cast<float>((lo >> (8 * b)) & 0xffu), x[8 * t + 2 * b], acc);
-                acc = fmaf(static_cast<float>((hi >> (8 * b)) & 0xffu), x[8 * t + 2 * b + 1], acc);
-            }
-        }
-    }
-    return acc;
-}
 
 template <Epilogue EP>
 __device__ __forceinline__ void store_out(float* y, int r, float d, float du) {
@@ -175,6 +120,10 @@ __global__ void __launch_bounds__(kThreads) matvec_fast(MatvecArgs a) {
                 s += chunk_dot<WT>(v[i][k], xr + k * F::CPC);
                 if constexpr (GLU) su += chunk_dot<WT>(vu[i][k], xr + k * F::CPC);
             }
+            if constexpr (WT == WType::INT8) {
+                s -= kBias<WT> * xsum;
+                if constexpr (GLU) su -= kBias<WT> * xsum;
+            }
             if constexpr (WT == WType::INT4) {
                 // One 128-column group per lane: lanes 4g..4g+3 share scale g of the slice.
                 const int r = min(r0 + i, out_rows - 1);
@@ -263,15 +212,18 @@ __global__ void __launch_bounds__(kThreads) matvec_generic(MatvecArgs a) {
             const char* p = static_cast<const char*>(a.w) + static_cast<size_t>(r) * rb + c * 16;
             float t = chunk_dot<WT>(load_stream(p), x);
             float tu = GLU ? chunk_dot<WT>(load_stream(p + static_cast<size_t>(out_rows) * rb), x) : 0.f;
-            if constexpr (WT == WType::INT4) {
+            if constexpr (WT != WType::BF16) {
                 float xsum = 0.f;
 #pragma unroll
                 for (int j = 0; j < F::CPC; ++j) xsum += x[j];
+                t -= kBias<WT> * xsum;
+                if constexpr (GLU) tu -= kBias<WT> * xsum;
+            }
+            if constexpr (WT == WType::INT4) {
                 const uint16_t* sc = static_cast<const uint16_t*>(a.scales);
                 const int gi = c * F::CPC / 128;
-                t = half_bits_to_float(sc[static_cast<size_t>(r) * groups_per_row + gi]) * (t - 8.f * xsum);
-                if constexpr (GLU)
-                    tu = half_bits_to_float(sc[static_cast<size_t>(r + out_rows) * groups_per_row + gi]) * (tu - 8.f * xsum);
+                t *= half_bits_to_float(sc[static_cast<size_t>(r) * groups_per_row + gi]);
+                if constexpr (GLU) tu *= half_bits_to_float(sc[static_cast<size_t>(r + out_rows) * groups_per_row + gi]);
             }
             s += t;
             su += tu;

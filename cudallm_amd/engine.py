@@ -53,6 +53,7 @@ SIGNATURES = {
     "cudallm_pos": ([c_void_p], c_int),
     "cudallm_step": ([c_void_p, c_int, _FP, _IP], c_int),
     "cudallm_step_debug": ([c_void_p, c_int, _FP, _FP, _IP], c_int),
+    "cudallm_step_profile": ([c_void_p, c_int, POINTER(c_ulonglong), ctypes.c_longlong, _IP], c_int),
     "cudallm_kernel_matvec": ([c_int, c_int, c_int, c_int, c_int, c_void_p, c_ulonglong, c_void_p, c_ulonglong,
                                _FP, _FP, c_float, _FP, c_int, c_int], c_int),
     "cudallm_kernel_rmsnorm": ([_FP, _FP, c_float, _FP, c_int], c_int),
@@ -166,6 +167,16 @@ class Engine:
         _check(_lib().cudallm_step_debug(self._handle(), -1 if token is None else int(token), _fp(residuals),
                                          _fp(logits), ctypes.byref(nxt)))
         return nxt.value, logits, residuals
+
+    def step_profile(self, token: int | None = None) -> np.ndarray:
+        """One synchronous step of the persistent kernel; returns uint64 stamps [grid, 128]
+        (100 MHz clock): [:, 0] start, [:, 1 + 6*l + k] end of phase k of layer l, [:, 97] lm_head."""
+        cap = 4096 * 128
+        buf = np.zeros(cap, dtype=np.uint64)
+        grid = c_int(0)
+        _check(_lib().cudallm_step_profile(self._handle(), -1 if token is None else int(token),
+                                           buf.ctypes.data_as(POINTER(c_ulonglong)), cap, ctypes.byref(grid)))
+        return buf[:grid.value * 128].reshape(grid.value, 128)
 
     def close(self) -> None:
         if self._h is not None:

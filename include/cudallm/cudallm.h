@@ -71,6 +71,16 @@ int  cudallm_step(cudallm_engine* e, int token, float* logits_out, int* next_tok
  * receives (n_layers+1)*hidden floats: after the embedding and after each layer. */
 int  cudallm_step_debug(cudallm_engine* e, int token, float* residuals_out, float* logits_out, int* next_token_out);
 
+/* One decode step (like cudallm_step with no outputs, but synchronous and never from the graph)
+ * that also records when each workgroup of the persistent decode kernel finished each phase.
+ * No reference counterpart: the reference profiled from outside with nsys.  stamps_out receives
+ * grid x 128 values of the GPU's 100 MHz real-time clock, per workgroup: [0] start,
+ * [1 + 6*layer + k] end of phase k (0 qkv, 1 attention, 2 split merge, 3 wo, 4 gate_up, 5 down),
+ * [97] lm_head end, [98] argmax end (workgroup 0); capacity >= grid * 128.  CUDALLM_ERR_STATE if the
+ * engine's options do not select the persistent kernel. */
+int  cudallm_step_profile(cudallm_engine* e, int token, unsigned long long* stamps_out, long long capacity,
+                          int* grid_out);
+
 /* ---- single-kernel test hooks: host pointers in/out; allocate, copy, run, copy back, free ----
  * Reference cudallm.h:44-56 / cudallm_capi.cpp:179-316. */
 
