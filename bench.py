@@ -10,10 +10,13 @@ drained on both sides; each step is one replay of the captured hipGraph with the
 the device (no host sync inside the timed region, as reference src/tools/cudallm_bench.cpp:64-80).
 
 Printed last, on one line: the JSON record.  ``value`` is bf16 decode tok/s; ``decode`` holds all
-three weight types; ``roofline`` is the dominant kernel (the fused RMSNorm + gate_up + SwiGLU
-matvec, 16 launches per token) timed live with HIP events on the launching stream over rotating
-weight copies (> 1 GiB, so the 256 MB Infinity Cache cannot serve them); ``cpu_baseline`` is the
-CPU oracle (the reference's algorithm restated, oracle/model.py) timed on this host.
+three weight types; ``roofline`` is the dominant kernel, the persistent decode kernel (one launch
+per token), timed live with HIP events recorded on the engine's stream around the K timed steps,
+with bytes per launch = weight bytes + the KV bytes the step reads, and ``traffic`` from the
+committed rocprofv3 counter summary (profiles/hbm_traffic.json); ``matvec_roofline`` is the
+standalone fused RMSNorm + gate_up + SwiGLU matvec over rotating weight copies (> 1 GiB, so the
+256 MB Infinity Cache cannot serve them); ``cpu_baseline`` is the CPU oracle (the reference's
+algorithm restated, oracle/model.py) timed on this host.
 """
 import argparse
 import json
@@ -57,11 +60,17 @@ def bench_decode(path, wd: str, steps: int, warmup: int, torch) -> dict:
         for _ in range(warmup):
             eng.step_async(None)
         torch.cuda.synchronize()
+        # HIP events on the engine's own stream, where each step is one graph replay of the decode kernel.
+        es = torch.cuda.ExternalStream(eng.stream)
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         t0 = time.perf_counter()
+        ev0.record(es)
         for _ in range(steps):
             eng.step_async(None)
+        ev1.record(es)
         torch.cuda.synchronize()
         dt = time.perf_counter() - t0
+        ev_us = ev0.elapsed_time(ev1) * 1e3 / steps
         nxt, _ = eng.step(None)
     ctx0 = PROMPT + warmup
     kv = KV_BYTES_PER_POS * (ctx0 + (steps + 1) // 2)  # reference cudallm_bench.cpp:82-85 accounting
@@ -70,7 +79,7 @@ def bench_decode(path, wd: str, steps: int, warmup: int, torch) -> dict:
     return {"tok_s": tok_s, "ms_per_token": 1e3 * dt / steps, "weight_bytes": weight_bytes, "bytes_per_token": bpt,
             "gbps": bpt * tok_s / 1e9, "frac_of_8tbs": bpt * tok_s / PEAK_HBM,
             "roofline_tok_s": PEAK_HBM / bpt, "context": [ctx0, ctx0 + steps], "load_s": round(load_s, 2),
-            "last_token": nxt}
+            "last_token": nxt, "kernel_avg_us": ev_us, "kernel_gbps": bpt / ev_us / 1e3}
 
 
 SHAPES = [("qkv", 3072, 2048, "store", True), ("wo", 2048, 2048, "add", False),
@@ -138,6 +147,34 @@ def bench_matvec(wd: str, name: str, rows: int, cols: int, ep: str, norm: bool, 
             "copies": copies}
 
 
+TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic.json"
+
+
+def traffic_bytes(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 counter summary: FETCH_SIZE and
+    WRITE_SIZE (KiB per dispatch), each scaled by what the same counter read for a device copy of
+    known size.  None when the summary has no entry for the kernel."""
+    try:
+        t = json.loads(TRAFFIC_FILE.read_text())
+        k, c = t["kernels"][kernel], t["copy_calibration"]
+    except (OSError, KeyError, ValueError):
+        return None
+    f_fac = c["bytes"] / (c["fetch_kib"] * 1024.0)
+    w_fac = c["bytes"] / (c["write_kib"] * 1024.0)
+    return round(k["fetch_kib"] * 1024.0 * f_fac + k["write_kib"] * 1024.0 * w_fac)
+
+
+def copy_calibration(mib: int, torch) -> None:
+    """Three device copies of `mib` MiB, so a counter run can scale its byte counters."""
+    a = torch.empty(mib << 20, dtype=torch.uint8, device="cuda").fill_(1)
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    del a, b
+    torch.cuda.empty_cache()
+
+
 def cpu_baseline(path, budget_s: float) -> dict:
     """The reference's CPU path (restated in oracle/model.py: fp32 dequantise per matmul, fp16 KV
     cache) decoding the same bf16 model on this host, for about `budget_s` seconds."""
@@ -187,6 +224,8 @@ def main() -> int:
     ap.add_argument("--no-kernels", action="store_true", help="skip the per-shape matvec lines")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--model-dir", default=None)
+    ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
+                    help="first run three device copies of MIB MiB (byte-counter calibration under rocprofv3)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (batch-1 decode does not shard across GPUs here); "
@@ -202,6 +241,8 @@ def main() -> int:
         print("bench.py: no GPU visible", file=sys.stderr)
         return 1
     torch.cuda.set_device(0)
+    if args.copy_calib:
+        copy_calibration(args.copy_calib, torch)
     dtypes = [d for d in args.dtypes.split(",") if d]
     base = args.model_dir or ("/dev/shm" if os.path.isdir("/dev/shm") else None)
     tmp = tempfile.TemporaryDirectory(dir=base)
@@ -214,7 +255,8 @@ def main() -> int:
         log(f"[bench] wrote {wd} model in {time.perf_counter() - t0:.1f} s")
         decode[wd] = bench_decode(paths[wd], wd, args.steps, args.warmup, torch)
         log(f"[bench] decode {wd}: {decode[wd]['tok_s']:.1f} tok/s, {decode[wd]['gbps']:.0f} GB/s "
-            f"({100 * decode[wd]['frac_of_8tbs']:.1f} % of 8 TB/s)")
+            f"({100 * decode[wd]['frac_of_8tbs']:.1f} % of 8 TB/s); kernel {decode[wd]['kernel_avg_us']:.1f} us "
+            f"by events")
         if wd != "bf16" or args.no_cpu:
             paths[wd].unlink()
 
@@ -250,10 +292,15 @@ def main() -> int:
                                f"+ {args.steps} timed steps, hipGraph replay (BASELINE config 5)",
                    "model": "llama-3.2-1b-shaped (random init)", "global_batch": 1,
                    "seq_len": PROMPT + args.warmup + args.steps, "parallelism": "none (1 GPU)"},
-        "roofline": {"bound": "hbm", "achieved": round(dom["gbps"], 1), "peak": 8000.0, "unit": "GB/s",
-                     "frac": round(dom["frac_of_8tbs"], 4), "traffic": None,
-                     "kernel": f"matvec_fast<{head_wd}, SWIGLU, norm> gate_up 16384x2048",
-                     "bytes_per_launch": dom["bytes"], "avg_us": round(dom["avg_us"], 3)},
+        "roofline": {"bound": "hbm", "achieved": round(head["kernel_gbps"], 1), "peak": 8000.0, "unit": "GB/s",
+                     "frac": round(head["kernel_gbps"] / 8000.0, 4), "traffic": traffic_bytes(f"decode_kernel<{head_wd}>"),
+                     "kernel": f"decode_kernel<{head_wd}> (persistent: the whole decode step is this one launch)",
+                     "bytes_per_launch": head["bytes_per_token"], "avg_us": round(head["kernel_avg_us"], 3),
+                     "timing": "HIP events on the engine's stream around the timed steps",
+                     "traffic_source": TRAFFIC_FILE.name},
+        "matvec_roofline": {"kernel": f"matvec_fast<{head_wd}, SWIGLU, norm> gate_up 16384x2048 (standalone)",
+                            "achieved": round(dom["gbps"], 1), "frac": round(dom["frac_of_8tbs"], 4),
+                            "bytes_per_launch": dom["bytes"], "avg_us": round(dom["avg_us"], 3)},
         "cpu_baseline": cpu,
         "decode": {wd: {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
                    for wd, r in decode.items()},

@@ -200,6 +200,13 @@ int cudallm_step_profile(cudallm_engine* e, int token, unsigned long long* stamp
     });
 }
 
+int cudallm_get_stream(cudallm_engine* e, void** stream_out) {
+    return guarded([&] {
+        CLLM_REQUIRE(e && e->impl && stream_out, "cudallm_get_stream: null argument");
+        *stream_out = e->impl->stream();
+    });
+}
+
 int cudallm_kernel_matvec(int impl, int weight_dtype, int epilogue, int fuse_norm, int rpb, const void* w,
                           unsigned long long w_bytes, const void* scales, unsigned long long scales_bytes,
                           const float* x, const float* norm_w, float eps, float* y, int rows, int cols) {

@@ -17,6 +17,10 @@ struct FormatError : std::runtime_error { using std::runtime_error::runtime_erro
 struct IoError : std::runtime_error { using std::runtime_error::runtime_error; };
 struct DeviceError : std::runtime_error { using std::runtime_error::runtime_error; };
 struct StateError : std::runtime_error { using std::runtime_error::runtime_error; };
+// A step on a full sequence.  The reference raises a plain runtime_error here
+// (src/engine/engine.cpp:118 via CUDALLM_CHECK), which its C ABI reports as CUDALLM_ERR_INTERNAL
+// (src/capi/cudallm_capi.cpp:22-29); this type keeps that code.
+struct SequenceFull : std::runtime_error { using std::runtime_error::runtime_error; };
 
 [[noreturn]] void throw_hip(hipError_t err, const char* expr, const char* file, int line);
 

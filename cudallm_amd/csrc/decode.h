@@ -55,7 +55,8 @@ struct DecodeParams {
 
 // Timestamp slots per workgroup: 0 = start, 1 + 6 l + k = end of phase k of layer l
 // (k: 0 qkv, 1 attention, 2 split merge, 3 wo, 4 gate_up, 5 down), 97 = lm_head end,
-// 98 = final argmax end (workgroup 0 only).
+// 98 = final argmax end (workgroup 0 only); for layer 1, 100 + 2 k = phase k's input arrived and
+// 101 + 2 k = its prologue done.
 constexpr int kStampSlots = 128;
 
 constexpr int kDecodeThreads = 256;

@@ -180,7 +180,7 @@ void Engine::reset() {
 }
 
 void Engine::step(int token, float* logits_out, int* next_token_out) {
-    if (host_pos_ >= max_seq_) throw StateError("step: the sequence is full (pos == max_seq_len); call reset()");
+    if (host_pos_ >= max_seq_) throw SequenceFull("step: the sequence is full (pos == max_seq_len); call reset()");
     CLLM_REQUIRE(token >= -1 && token < config().vocab, "step: token out of range");
     if (token >= 0) launch_set_token(d_token_, token, stream_);
     if (opts_.graph) {
@@ -217,7 +217,7 @@ void Engine::step(int token, float* logits_out, int* next_token_out) {
 }
 
 void Engine::step_debug(int token, float* residuals_out, float* logits_out, int* next_token_out) {
-    if (host_pos_ >= max_seq_) throw StateError("step_debug: the sequence is full (pos == max_seq_len); call reset()");
+    if (host_pos_ >= max_seq_) throw SequenceFull("step_debug: the sequence is full (pos == max_seq_len); call reset()");
     CLLM_REQUIRE(token >= -1 && token < config().vocab, "step_debug: token out of range");
     CLLM_REQUIRE(residuals_out, "step_debug: residuals_out is null");
     if (token >= 0) launch_set_token(d_token_, token, stream_);
@@ -241,7 +241,7 @@ void Engine::step_debug(int token, float* residuals_out, float* logits_out, int*
 
 int Engine::step_profile(int token, unsigned long long* stamps_out, long capacity) {
     if (!persistent_) throw StateError("step_profile: this engine does not use the persistent decode kernel");
-    if (host_pos_ >= max_seq_) throw StateError("step_profile: the sequence is full (pos == max_seq_len); call reset()");
+    if (host_pos_ >= max_seq_) throw SequenceFull("step_profile: the sequence is full (pos == max_seq_len); call reset()");
     CLLM_REQUIRE(token >= -1 && token < config().vocab, "step_profile: token out of range");
     CLLM_REQUIRE(stamps_out && capacity >= static_cast<long>(grid_) * kStampSlots,
                  "step_profile: stamps_out must hold grid * 128 values");

@@ -42,6 +42,7 @@ public:
     void step_debug(int token, float* residuals_out, float* logits_out, int* next_token_out);
     // One step of the persistent kernel with per-phase timestamps; returns the grid size.
     int step_profile(int token, unsigned long long* stamps_out, long capacity);
+    hipStream_t stream() const { return stream_; }
 
 private:
     void enqueue_forward(float* residuals_out);

@@ -238,6 +238,11 @@ __device__ __forceinline__ float embed(const void* w, const void* s, int tok, in
 __device__ __forceinline__ void stamp(const DecodeParams& p, int slot) {
     if (p.stamps && threadIdx.x == 0) p.stamps[blockIdx.x * kStampSlots + slot] = __builtin_amdgcn_s_memrealtime();
 }
+// In-phase timestamp, recorded for layer 1 only (slots kInPhase + 2 * phase + {0: input arrived, 1: prologue done}).
+constexpr int kInPhase = 100;
+__device__ __forceinline__ void stamp_in(const DecodeParams& p, int l, int phase, int k) {
+    if (l == 1) stamp(p, kInPhase + 2 * phase + k);
+}
 
 // Argmax order: larger value first, then lower index (numpy's tie rule).  NaN never wins.
 __device__ __forceinline__ bool arg_better(float v, int i, float bv, int bi) { return v > bv || (v == bv && i < bi); }
@@ -346,9 +351,11 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
                 }
             }
             if (l > 0) fetch<H>(p.tx + static_cast<size_t>(l) * H, tg - kTagStride + T_X, xin, err, tid);
+            stamp_in(p, l, 0, 0);
             const float inv = rms_inv(xin, p.eps, scratch, tid);
             float xr[NX], xsum;
             lane_inputs<WT, true>(xin, Lw.attn_norm, inv, xr, xsum, lane);
+            stamp_in(p, l, 0, 1);
             auto finish = [&](int u, float d0, float d1) {
                 const int h = u / 32, i = u % 32, r0 = h * HD + i;
                 float o0 = d0, o1 = d1;
@@ -418,6 +425,7 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
                 if (tid < 2 * HD && t0 + n - 1 == pos)
                     kvc[tid] = wait1(tqkv + (tid < HD ? NH * HD : (NH + NKV) * HD - HD) + kvh * HD + tid, tg + T_QKV, err);
                 __syncthreads();
+                if (t == static_cast<int>(blockIdx.x)) stamp_in(p, l, 1, 0);
 #pragma unroll
                 for (int k = 0; k < kTile; ++k) {
                     const int idx = tid + k * kThreads, r = idx / 8, c = idx % 8;
@@ -532,8 +540,10 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
             for (int i = 0; i < kWoU; ++i)
                 if (gw + i * NW < H) load_row<WT>(Lw.wo, Lw.so, gw + i * NW, lane, rw[i]);
             fetch<H>(tatt, tg + T_ATT, big, err, tid);
+            stamp_in(p, l, 3, 0);
             float xr[NX], xsum;
             lane_inputs<WT, false>(big, nullptr, 1.f, xr, xsum, lane);
+            stamp_in(p, l, 3, 1);
 #pragma unroll
             for (int i = 0; i < kWoU; ++i) {
                 const int r = gw + i * NW;
@@ -567,9 +577,11 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
                 }
             }
             fetch<H>(txa, tg + T_XA, xa, err, tid);
+            stamp_in(p, l, 4, 0);
             const float inv = rms_inv(xa, p.eps, scratch, tid);
             float xr[NX], xsum;
             lane_inputs<WT, true>(xa, Lw.ffn_norm, inv, xr, xsum, lane);
+            stamp_in(p, l, 4, 1);
 #pragma unroll
             for (int i = 0; i < kGuU; ++i) {
                 const int u = gw + i * NW;
@@ -605,6 +617,7 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
             for (int i = 0; i < PD; ++i)
                 if (gw + i * NW < H) load_drow<WT>(Lw.wd, Lw.sd, gw + i * NW, lane, rd[i]);
             fetch<INTER>(tact, tg + T_ACT, big, err, tid);
+            stamp_in(p, l, 5, 0);
             auto finish = [&](int r, float d) {
                 const float xn = xa[r] + d;
                 tstore(txo + r, xn, tg + T_X);

@@ -51,6 +51,7 @@ SIGNATURES = {
     "cudallm_get_config": ([c_void_p, POINTER(CudallmConfigInfo)], c_int),
     "cudallm_reset": ([c_void_p], c_int),
     "cudallm_pos": ([c_void_p], c_int),
+    "cudallm_get_stream": ([c_void_p, POINTER(c_void_p)], c_int),
     "cudallm_step": ([c_void_p, c_int, _FP, _IP], c_int),
     "cudallm_step_debug": ([c_void_p, c_int, _FP, _FP, _IP], c_int),
     "cudallm_step_profile": ([c_void_p, c_int, POINTER(c_ulonglong), ctypes.c_longlong, _IP], c_int),
@@ -177,6 +178,13 @@ class Engine:
         _check(_lib().cudallm_step_profile(self._handle(), -1 if token is None else int(token),
                                            buf.ctypes.data_as(POINTER(c_ulonglong)), cap, ctypes.byref(grid)))
         return buf[:grid.value * 128].reshape(grid.value, 128)
+
+    @property
+    def stream(self) -> int:
+        """Address of the engine's HIP stream (hipStream_t), e.g. for torch.cuda.ExternalStream."""
+        s = c_void_p(0)
+        _check(_lib().cudallm_get_stream(self._handle(), ctypes.byref(s)))
+        return s.value or 0
 
     def close(self) -> None:
         if self._h is not None:

@@ -76,10 +76,17 @@ int  cudallm_step_debug(cudallm_engine* e, int token, float* residuals_out, floa
  * No reference counterpart: the reference profiled from outside with nsys.  stamps_out receives
  * grid x 128 values of the GPU's 100 MHz real-time clock, per workgroup: [0] start,
  * [1 + 6*layer + k] end of phase k (0 qkv, 1 attention, 2 split merge, 3 wo, 4 gate_up, 5 down),
- * [97] lm_head end, [98] argmax end (workgroup 0); capacity >= grid * 128.  CUDALLM_ERR_STATE if the
+ * [97] lm_head end, [98] argmax end (workgroup 0); for layer 1 only, [100 + 2k] when phase k's input had
+ * arrived and [101 + 2k] when its prologue was done; capacity >= grid * 128.  CUDALLM_ERR_STATE if the
  * engine's options do not select the persistent kernel. */
 int  cudallm_step_profile(cudallm_engine* e, int token, unsigned long long* stamps_out, long long capacity,
                           int* grid_out);
+
+/* The HIP stream (a hipStream_t) on which the engine enqueues every step.  No reference
+ * counterpart (the reference's stream is private to its Engine, src/engine/engine.cpp:40): it lets
+ * a caller order its own device work after the engine's, or time steps with HIP events recorded
+ * on this stream.  The stream belongs to the engine and dies with it. */
+int  cudallm_get_stream(cudallm_engine* e, void** stream_out);
 
 /* ---- single-kernel test hooks: host pointers in/out; allocate, copy, run, copy back, free ----
  * Reference cudallm.h:44-56 / cudallm_capi.cpp:179-316. */

@@ -64,6 +64,8 @@ def test_null_arguments(lib):
     assert lib.cudallm_reset(None) == INVALID_ARG
     assert lib.cudallm_step(None, 0, None, None) == INVALID_ARG
     assert lib.cudallm_get_config(None, None) == INVALID_ARG
+    s = ctypes.c_void_p(0)
+    assert lib.cudallm_get_stream(None, ctypes.byref(s)) == INVALID_ARG and s.value is None
     lib.cudallm_destroy(None)
 
 
