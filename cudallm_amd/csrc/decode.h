@@ -59,7 +59,7 @@ struct DecodeParams {
 // 101 + 2 k = its prologue done.
 constexpr int kStampSlots = 128;
 
-constexpr int kDecodeThreads = 256;
+constexpr int kDecodeThreads = 512;  // 4 compute waves + 4 loader waves
 
 // Enqueue one decode step (one launch).  `grid` workgroups must all be co-resident.
 void launch_decode(WType wt, const DecodeParams& p, int grid, hipStream_t s);

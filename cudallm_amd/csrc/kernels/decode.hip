@@ -6,16 +6,23 @@
 // the final RMSNorm; argmax that writes the token and advances the position).  How it is
 // scheduled is this file's own:
 //
-//  * One workgroup of 4 waves per CU (one wave per SIMD, so each wave may use 512 registers and
-//    the prefetched weight rows never go to scratch); every workgroup runs every phase.  Matvec
-//    rows are dealt to waves round-robin, attention splits to workgroups.
+//  * One workgroup of 8 waves per CU, every workgroup running every phase.  Waves 0-3 compute;
+//    wave 4 + w is the loader of compute wave w.  Matvec rows are dealt to compute waves
+//    round-robin, attention splits to workgroups.
+//  * The rows a compute wave will multiply are fixed by its index alone, so its loader walks that
+//    whole schedule (every phase of every layer, then lm_head) from the first instruction of the
+//    step and streams the rows as 1 KiB lines (64 lanes x 16 B) into the compute wave's LDS ring,
+//    running ahead across phase boundaries; it only ever waits for ring space.  HBM therefore
+//    keeps streaming while compute waves wait for the inputs of their next phase.  The loader
+//    keeps kNB lines in flight with ordinary 128-bit loads and copies each landed line into the
+//    ring; quantised lines carry one 32-bit side value per lane (row scale or group scale).
 //  * Phases exchange vectors through tagged 64-bit words (see decode.h).  A consumer loads the
 //    vector it needs with relaxed agent-scope atomics and re-loads only entries whose tag is not
-//    yet the current phase's.  No grid barriers, no RMW atomics and no cache flushes on the data
-//    path: the dependency chain costs one store->load hop per phase.
-//  * A wave issues the weight loads of its first rows (and their scales) BEFORE it waits for the
-//    phase input, so the HBM stream continues while the producing phase finishes elsewhere; the
-//    attention workgroups likewise pull their K/V tiles before waiting for q.
+//    yet the current phase's.  Compute waves issue no weight loads, so these polls are never
+//    queued behind a weight stream.  No grid barriers, no RMW atomics and no cache flushes on the
+//    data path: the dependency chain costs one store->load hop per phase.
+//  * The four compute waves synchronise among themselves with an LDS epoch barrier (the loaders
+//    run their own schedule and never join a workgroup barrier).
 //  * Every wait is bounded.  On overrun the wave sets the sticky d_err flag and continues with
 //    whatever it read; other waits notice the flag and stop waiting, so the grid always drains.
 //    Indices never depend on activation values and the token is clamped, so no access can leave
@@ -33,37 +40,89 @@ using mv::chunk_dot;
 using mv::kBias;
 using mv::row_bytes;
 
-constexpr int kThreads = kDecodeThreads, kWaves = kThreads / kWave;
+constexpr int kCW = 4;                  // compute waves per workgroup (loaders are waves kCW..2kCW-1)
+constexpr int kThreads = kDecodeThreads;
+constexpr int kCT = kCW * kWave;        // compute threads
+static_assert(kThreads == 2 * kCT, "one loader wave per compute wave");
 constexpr int H = 2048, INTER = 8192, NH = 32, NKV = 8, HD = 64, QKV = (NH + 2 * NKV) * HD, VOCAB = 128256, NL = 16;
 constexpr int kTagStride = 8;            // tag slots per layer
 constexpr unsigned kEpochStride = 256;   // tag slots per step
 constexpr unsigned kSpinCap = 1u << 20;  // bounded waits (~1 s of polling)
 constexpr int kPartStride = HD + 2;      // o[64], m, l
 constexpr int kPairs = QKV / 2;          // RoPE pairs (i, i+32) of every q/k/v head
-// Units per wave when the grid has 256 workgroups (1024 waves); smaller grids loop further.
-constexpr int kNW = 256 * kWaves;
-constexpr int kQkvU = (kPairs + kNW - 1) / kNW;  // 2 pairs
-constexpr int kWoU = (H + kNW - 1) / kNW;        // 2 rows
-constexpr int kGuU = (INTER + kNW - 1) / kNW;    // 8 gate/up units
-constexpr int kDownU = (H + kNW - 1) / kNW;      // 2 rows
+constexpr int kLmR = 2;                  // lm_head rows per unit
+constexpr int kNB = 8;                   // lines in flight per loader wave
+static_assert(VOCAB % kLmR == 0, "lm_head units");
 
 enum : unsigned { T_QKV = 0, T_ATT_PART = 1, T_ATT = 2, T_XA = 3, T_ACT = 4, T_X = 5 };
 constexpr unsigned T_ARG = NL * kTagStride;
 
+// Ring geometry per weight type.
+template <WType WT>
+struct RingCfg {
+    static constexpr bool kQuant = WT != WType::BF16;
+    static constexpr int S = kQuant ? 20 : 24;                 // 1 KiB slots per compute wave
+    static constexpr int SS = kQuant ? S : 1;                  // side-value slots
+    static constexpr int LPR2 = Fmt<WT>::CPL;                  // lines per 2048-wide row
+    static constexpr int LPR8 = INTER / Fmt<WT>::CPC / kWave;  // lines per 8192-wide row
+};
+
+template <WType WT>
+struct Smem {
+    u32x4 ring[kCW][RingCfg<WT>::S][kWave];
+    float side[kCW][RingCfg<WT>::SS][kWave];
+    float xin[H];     // layer input (residual stream)
+    float xa[H];      // residual after attention
+    float big[9216];  // attention tiles | attention output | SwiGLU output
+    float rope_c[HD / 2], rope_s[HD / 2];
+    float part[kCW];
+    float red_v[kCW];
+    int red_i[kCW];
+    unsigned bar[kCW];
+    int full[kCW];  // lines the loader has published, per compute wave
+    int done[kCW];  // lines the compute wave has released
+};
+
+// ---- cross-workgroup tagged words ------------------------------------------------------------
+
+// Every device pointer in DecodeParams is global memory; saying so keeps the accesses off the
+// flat path (which would also count against the LDS counter).
+template <typename T>
+__device__ __forceinline__ __attribute__((address_space(1))) T* glob(T* p) {
+    return (__attribute__((address_space(1))) T*)p;
+}
+
+// The layer's weight pointers (field by field: a struct copy cannot read another address space).
+__device__ __forceinline__ DecodeLayer load_layer(const DecodeLayer* t, int l) {
+    const __attribute__((address_space(1))) DecodeLayer* g = glob(t + l);
+    DecodeLayer L;
+    L.attn_norm = g->attn_norm;
+    L.wqkv = g->wqkv;
+    L.sqkv = g->sqkv;
+    L.wo = g->wo;
+    L.so = g->so;
+    L.ffn_norm = g->ffn_norm;
+    L.wgu = g->wgu;
+    L.sgu = g->sgu;
+    L.wd = g->wd;
+    L.sd = g->sd;
+    return L;
+}
+
 __device__ __forceinline__ uint64_t tload(const uint64_t* a) {
-    return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return __hip_atomic_load(glob(a), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void tstore(uint64_t* a, float v, unsigned tag) {
-    __hip_atomic_store(a, (static_cast<uint64_t>(tag) << 32) | __builtin_bit_cast(uint32_t, v), __ATOMIC_RELAXED,
+    __hip_atomic_store(glob(a), (static_cast<uint64_t>(tag) << 32) | __builtin_bit_cast(uint32_t, v), __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ bool tagged(uint64_t v, unsigned tag) { return static_cast<unsigned>(v >> 32) == tag; }
 __device__ __forceinline__ float tvalue(uint64_t v) { return __builtin_bit_cast(float, static_cast<uint32_t>(v)); }
 __device__ __forceinline__ bool failed(unsigned* err) {
-    return __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
+    return __hip_atomic_load(glob(err), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
 }
 __device__ __forceinline__ void fail(unsigned* err) {
-    __hip_atomic_fetch_or(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_fetch_or(glob(err), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 // True when a wait must stop: it ran out of polls, or another wave already failed.
 __device__ __forceinline__ bool give_up(unsigned& spins, unsigned* err) {
@@ -83,14 +142,221 @@ __device__ __forceinline__ float wait1(const uint64_t* a, unsigned tag, unsigned
     return tvalue(v);
 }
 
-// The whole workgroup copies N tagged floats into LDS once every tag equals `tag`.
-template <int N>
-__device__ void fetch(const uint64_t* src, unsigned tag, float* dst, unsigned* err, int tid) {
-    constexpr int PT = N / kThreads;
-    static_assert(N % kThreads == 0, "fetch size");
+// ---- workgroup-local synchronisation (LDS) ---------------------------------------------------
+
+__device__ __forceinline__ int lds_load(int* a) { return __hip_atomic_load(a, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP); }
+__device__ __forceinline__ void lds_store(int* a, int v) { __hip_atomic_store(a, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP); }
+
+// Barrier of the kCW compute waves: each publishes its epoch, then waits for all.  Orders the
+// LDS writes made before it against the reads made after it.
+__device__ __forceinline__ void cbar(unsigned* bar, unsigned& ep, int wave, int lane, unsigned* err) {
+    ++ep;
+    if (lane == 0) __hip_atomic_store(bar + wave, ep, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+    unsigned spins = 0;
+    for (;;) {
+        unsigned lo = ~0u;
+#pragma unroll
+        for (int w = 0; w < kCW; ++w) lo = min(lo, __hip_atomic_load(bar + w, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP));
+        if (lo >= ep || give_up(spins, err)) break;
+    }
+}
+
+// Wait until the loader has published `need` lines of this wave's ring.
+__device__ __forceinline__ void ring_wait(int need, int& cfull, int* full, unsigned* err) {
+    if (cfull >= need) return;
+    unsigned spins = 0;
+    for (;;) {
+        cfull = lds_load(full);
+        if (cfull >= need || give_up(spins, err)) break;
+    }
+}
+
+// ---- the loader ------------------------------------------------------------------------------
+
+// Walks a compute wave's weight rows in the order the compute code multiplies them: per layer the
+// segments qkv (RoPE pairs: rows r and r+32), wo, gate_up (gate row u, up row u+inter), down
+// (8192-wide rows); then lm_head (kLmR consecutive rows per unit).  Unit u of a segment belongs to
+// compute wave gw when u = gw (mod NW).  With NW a multiple of 32 the rows of consecutive units
+// of a wave are a fixed stride apart in every segment, so a line advance is pointer arithmetic.
+// All state is wave-uniform.
+template <WType WT>
+struct Stream {
+    using C = RingCfg<WT>;
+    static constexpr size_t kScB = WT == WType::INT4 ? 2 : 4;  // bytes per scale
+    const DecodeParams* p;
+    int gw, NW;
+    int l = 0, seg = 0;
+    bool have = false, end = false;
+    int lpr = 1, rpu = 1;   // lines per row, rows per unit
+    int lc = 0, rl = 0, ul = 0;  // lines left in the row, rows left in the unit, units left
+    const char *cur = nullptr, *rowp = nullptr, *unitp = nullptr;     // weight line / row / unit
+    const char *scur = nullptr, *srowp = nullptr, *sunitp = nullptr;  // their side values
+    size_t kstr = 0, ustr = 0, skstr = 0, sustr = 0, sline = 0;
+
+    __device__ void set_seg() {
+        const char* mat;
+        const char* sc;
+        int N, r0, krows, urows, cols;
+        if (seg == 4) {
+            mat = static_cast<const char*>(p->emb);
+            sc = static_cast<const char*>(p->emb_s);
+            N = VOCAB / kLmR, r0 = gw * kLmR, krows = 1, urows = NW * kLmR, rpu = kLmR, cols = H;
+        } else {
+            const DecodeLayer L = load_layer(p->layers, l);
+            mat = static_cast<const char*>(seg == 0 ? L.wqkv : seg == 1 ? L.wo : seg == 2 ? L.wgu : L.wd);
+            sc = static_cast<const char*>(seg == 0 ? L.sqkv : seg == 1 ? L.so : seg == 2 ? L.sgu : L.sd);
+            N = seg == 0 ? kPairs : seg == 2 ? INTER : H;
+            r0 = seg == 0 ? (gw / 32) * HD + gw % 32 : gw;
+            krows = seg == 0 ? 32 : seg == 2 ? INTER : 0;
+            urows = seg == 0 ? 2 * NW : NW;
+            rpu = (seg == 0 || seg == 2) ? 2 : 1;
+            cols = seg == 3 ? INTER : H;
+        }
+        lpr = cols / Fmt<WT>::CPC / kWave;
+        const size_t rb = row_bytes<WT>(cols);
+        const size_t sb = WT == WType::INT4 ? (cols / 128) * kScB : kScB;  // side bytes per row
+        kstr = krows * rb, ustr = urows * rb;
+        skstr = krows * sb, sustr = urows * sb;
+        sline = WT == WType::INT4 ? 16 * kScB : 0;  // an int4 line spans 16 scale groups
+        unitp = rowp = cur = mat + static_cast<size_t>(r0) * rb;
+        sunitp = srowp = scur = sc + static_cast<size_t>(r0) * sb;
+        lc = lpr, rl = rpu, ul = (N - gw + NW - 1) / NW;
+        have = ul > 0;
+    }
+    // Next segment (each wave has units in every segment when NW <= kPairs).
+    __device__ void next_seg() {
+        if (seg == 4) {
+            end = true;
+            return;
+        }
+        if (seg == 3) {
+            if (l + 1 < NL) {
+                ++l;
+                seg = 0;
+            } else {
+                seg = 4;
+            }
+        } else {
+            ++seg;
+        }
+        set_seg();
+    }
+    __device__ void init(const DecodeParams* pp, int gw_, int nw) {
+        p = pp, gw = gw_, NW = nw, l = 0, seg = 0, end = false;
+        set_seg();
+    }
+    // Step past the current line within the segment; clears `have` at the segment's end.
+    __device__ __forceinline__ void advance() {
+        if (--lc > 0) {
+            cur += 1024;
+            scur += sline;
+            return;
+        }
+        lc = lpr;
+        if (--rl > 0) {
+            rowp += kstr;
+            srowp += skstr;
+        } else {
+            rl = rpu;
+            if (--ul == 0) {
+                have = false;
+                return;
+            }
+            unitp += ustr;
+            sunitp += sustr;
+            rowp = unitp;
+            srowp = sunitp;
+        }
+        cur = rowp;
+        scur = srowp;
+    }
+};
+
+template <WType WT>
+__device__ __forceinline__ float side_value(uint32_t raw) {
+    if constexpr (WT == WType::INT4) return half_bits_to_float(static_cast<uint16_t>(raw));
+    return __builtin_bit_cast(float, raw);
+}
+
+// Loader wave for compute wave `wave`: kNB lines in flight.  Every slot always holds a load (a
+// repeat of the last line where the stream has none, at a segment switch or past the end), so the
+// in-order completion count the compiler waits on is exact; each landed line is copied into the
+// ring and published through full[wave].  The segment switch runs once per round of kNB slots.
+template <WType WT>
+__device__ void loader(const DecodeParams& p, Smem<WT>& sm, int wave, int lane) {
+    using C = RingCfg<WT>;
+    unsigned* err = p.d_err;
+    const int gw = blockIdx.x * kCW + wave, NW = gridDim.x * kCW;
+    Stream<WT> st;
+    st.init(&p, gw, NW);
+    const int loff = lane * 16;
+    const int soff = WT == WType::INT4 ? (lane / 4) * 2 : 0;
+    u32x4 buf[kNB];
+    uint32_t sd[kNB];
+    bool v[kNB];
+    const char* last = st.cur;
+    const char* slast = st.scur;
+    auto issue = [&](int s) {
+        v[s] = st.have;
+        if (st.have) {
+            last = st.cur;
+            slast = st.scur;
+        }
+        buf[s] = load_stream(last + loff);
+        if constexpr (WT == WType::INT8) sd[s] = gload(reinterpret_cast<const uint32_t*>(slast));
+        if constexpr (WT == WType::INT4) sd[s] = gload(reinterpret_cast<const uint16_t*>(slast + soff));
+        if (st.have) st.advance();
+    };
+#pragma unroll
+    for (int s = 0; s < kNB; ++s) issue(s);
+    int k = 0, cdone = 0;
+    for (;;) {
+        bool any = false;
+#pragma unroll
+        for (int s = 0; s < kNB; ++s) {
+            if (v[s]) {
+                any = true;
+                if (k - cdone >= C::S) {
+                    unsigned spins = 0;
+                    for (;;) {
+                        cdone = lds_load(&sm.done[wave]);
+                        if (k - cdone < C::S || give_up(spins, err)) break;
+                    }
+                }
+                const int slot = k % C::S;
+                sm.ring[wave][slot][lane] = buf[s];
+                if constexpr (C::kQuant) sm.side[wave][slot][lane] = side_value<WT>(sd[s]);
+                ++k;
+                if (lane == 0) lds_store(&sm.full[wave], k);
+            }
+            issue(s);
+        }
+        if (!st.have && !st.end) st.next_seg();
+        if (!any && st.end) break;
+    }
+}
+
+// ---- compute-wave helpers --------------------------------------------------------------------
+
+// LDS position of element i of an 8192-wide input stored for the down projection: lane l of
+// 16-byte chunk c needs elements (64 c + l) CPC .. + CPC - 1, kept as [chunk][quad][lane] float4s
+// so the 64 lanes' 128-bit reads of one quad are consecutive (no bank conflicts).
+template <int CPC>
+__device__ __forceinline__ int swz(int i) {
+    const int c = i / (kWave * CPC), l = (i / CPC) % kWave, q = (i % CPC) / 4, e = i % 4;
+    return ((c * (CPC / 4) + q) * kWave + l) * 4 + e;
+}
+
+// The whole compute group copies N tagged floats into LDS once every tag equals `tag` (at swz<SWZ>
+// positions when SWZ > 0); with SQ, each wave also leaves the sum of squares of the values it
+// copied in part[wave].  Callers follow with cbar().
+template <int N, bool SQ, int SWZ = 0>
+__device__ void fetch(const uint64_t* src, unsigned tag, float* dst, float* part, unsigned* err, int tid) {
+    constexpr int PT = N / kCT;
+    static_assert(N % kCT == 0, "fetch size");
     uint64_t v[PT];
 #pragma unroll
-    for (int k = 0; k < PT; ++k) v[k] = tload(src + tid + k * kThreads);
+    for (int k = 0; k < PT; ++k) v[k] = tload(src + tid + k * kCT);
     unsigned spins = 0;
     for (;;) {
         bool ok = true;
@@ -99,26 +365,52 @@ __device__ void fetch(const uint64_t* src, unsigned tag, float* dst, unsigned* e
         if (ok || give_up(spins, err)) break;
 #pragma unroll
         for (int k = 0; k < PT; ++k)
-            if (!tagged(v[k], tag)) v[k] = tload(src + tid + k * kThreads);
+            if (!tagged(v[k], tag)) v[k] = tload(src + tid + k * kCT);
     }
+    float ss = 0.f;
 #pragma unroll
-    for (int k = 0; k < PT; ++k) dst[tid + k * kThreads] = tvalue(v[k]);
-    __syncthreads();
+    for (int k = 0; k < PT; ++k) {
+        const float x = tvalue(v[k]);
+        const int i = tid + k * kCT;
+        if constexpr (SWZ > 0) {
+            dst[swz<SWZ>(i)] = x;
+        } else {
+            dst[i] = x;
+        }
+        ss += x * x;
+    }
+    if constexpr (SQ) {
+        ss = wave_sum(ss);
+        if ((tid & (kWave - 1)) == 0) part[tid / kWave] = ss;
+    }
 }
 
-// 1 / rms(x), identical in every workgroup (same partition, same order).
-__device__ float rms_inv(const float* x, float eps, float* scratch, int tid) {
+// 1 / rms from the per-wave partial sums of squares (same partition and order in every workgroup).
+__device__ __forceinline__ float rms_inv(const float* part, float eps) {
     float ss = 0.f;
-    for (int j = tid; j < H; j += kThreads) ss += x[j] * x[j];
-    ss = block_sum(ss, scratch);
+#pragma unroll
+    for (int w = 0; w < kCW; ++w) ss += part[w];
     return rsqrtf(ss / static_cast<float>(H) + eps);
 }
 
-// The lane's 32 inputs of a 2048-wide row (same column mapping as the standalone matvec), scaled
-// by inv * norm_w when NORM.  norm_w is read with 128-bit global loads.
+// Norm weights of the lane's 32 columns of a 2048-wide row (same column mapping as the matvec).
 typedef const __attribute__((address_space(1))) f32x4 global_f32x4;
+template <WType WT>
+struct NormW {
+    f32x4 v[Fmt<WT>::CPL * Fmt<WT>::CPC / 4];
+};
+template <WType WT>
+__device__ __forceinline__ void load_norm(const float* w, int lane, NormW<WT>& n) {
+    using F = Fmt<WT>;
+#pragma unroll
+    for (int k = 0; k < F::CPL; ++k)
+#pragma unroll
+        for (int j = 0; j < F::CPC; j += 4) n.v[(k * F::CPC + j) / 4] = *((global_f32x4*)(w + (k * kWave + lane) * F::CPC + j));
+}
+
+// The lane's 32 inputs of a 2048-wide row, scaled by inv * norm_w when a norm is given.
 template <WType WT, bool NORM>
-__device__ __forceinline__ void lane_inputs(const float* x, const float* norm_w, float inv, float* xr, float& xsum,
+__device__ __forceinline__ void lane_inputs(const float* x, const NormW<WT>* nw, float inv, float* xr, float& xsum,
                                             int lane) {
     using F = Fmt<WT>;
     xsum = 0.f;
@@ -128,11 +420,10 @@ __device__ __forceinline__ void lane_inputs(const float* x, const float* norm_w,
 #pragma unroll
         for (int j = 0; j < F::CPC; j += 4) {
             const f32x4 xv = *reinterpret_cast<const f32x4*>(x + c0 + j);
-            f32x4 nw = {1.f, 1.f, 1.f, 1.f};
-            if constexpr (NORM) nw = *((global_f32x4*)(norm_w + c0 + j));
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const float v = NORM ? xv[e] * inv * nw[e] : xv[e];
+                float v = xv[e];
+                if constexpr (NORM) v = v * inv * nw->v[(k * F::CPC + j) / 4][e];
                 xr[k * F::CPC + j + e] = v;
                 xsum += v;
             }
@@ -140,23 +431,31 @@ __device__ __forceinline__ void lane_inputs(const float* x, const float* norm_w,
     }
 }
 
-// One 2048-wide weight row as this lane holds it: its 16-byte chunks and the scale it needs
-// (int8: the row scale; int4: the scale of the lane's 128-column group).
+// One 2048-wide row as this lane holds it: its 16-byte chunks and its side value.
 template <WType WT>
 struct Row {
     u32x4 w[Fmt<WT>::CPL];
     float s;
 };
 
+// Compute wave's view of its ring.
+struct Cons {
+    int k = 0;      // lines consumed
+    int cfull = 0;  // published lines last seen
+};
+
 template <WType WT>
-__device__ __forceinline__ void load_row(const void* w, const void* scales, int row, int lane, Row<WT>& r) {
-    const char* p = static_cast<const char*>(w) + static_cast<size_t>(row) * row_bytes<WT>(H) + lane * 16;
+__device__ __forceinline__ void take_row(Smem<WT>& sm, Cons& cs, int wave, int lane, unsigned* err, Row<WT>& r) {
+    using C = RingCfg<WT>;
+    ring_wait(cs.k + C::LPR2, cs.cfull, &sm.full[wave], err);
 #pragma unroll
-    for (int k = 0; k < Fmt<WT>::CPL; ++k) r.w[k] = load_stream(p + k * 1024);
-    if constexpr (WT == WType::INT8) r.s = gload(static_cast<const float*>(scales) + row);
-    if constexpr (WT == WType::INT4)
-        r.s = half_bits_to_float(
-            gload(static_cast<const uint16_t*>(scales) + static_cast<size_t>(row) * (H / 128) + lane / 4));
+    for (int c = 0; c < C::LPR2; ++c) r.w[c] = sm.ring[wave][(cs.k + c) % C::S][lane];
+    if constexpr (C::kQuant) r.s = sm.side[wave][cs.k % C::S][lane];
+    cs.k += C::LPR2;
+}
+template <WType WT>
+__device__ __forceinline__ void release(Smem<WT>& sm, const Cons& cs, int wave, int lane) {
+    if (lane == 0) lds_store(&sm.done[wave], cs.k);
 }
 
 // Complete dot of a 2048-wide row, uniform across the wave.
@@ -173,48 +472,55 @@ __device__ __forceinline__ float row_dot(const Row<WT>& r, const float* xr, floa
     return s;
 }
 
-// One 8192-wide row (down projection): DCH chunks per lane, inputs read from LDS.
+// Dot of one 8192-wide row (down projection) taken from the ring four lines at a time, inputs from
+// LDS in the swz layout.
 template <WType WT>
-struct DRow {
-    static constexpr int DCH = INTER / Fmt<WT>::CPC / kWave;
-    u32x4 w[DCH];
-    float s[WT == WType::INT4 ? DCH : 1];
-};
-
-template <WType WT>
-__device__ __forceinline__ void load_drow(const void* w, const void* scales, int row, int lane, DRow<WT>& r) {
-    constexpr int DCH = DRow<WT>::DCH;
-    const char* p = static_cast<const char*>(w) + static_cast<size_t>(row) * row_bytes<WT>(INTER) + lane * 16;
-#pragma unroll
-    for (int k = 0; k < DCH; ++k) r.w[k] = load_stream(p + k * 1024);
-    if constexpr (WT == WType::INT8) r.s[0] = gload(static_cast<const float*>(scales) + row);
-    if constexpr (WT == WType::INT4) {
-        const uint16_t* sc = static_cast<const uint16_t*>(scales) + static_cast<size_t>(row) * (INTER / 128);
-#pragma unroll
-        for (int k = 0; k < DCH; ++k) r.s[k] = half_bits_to_float(gload(sc + (k * kWave + lane) / 4));
-    }
-}
-
-template <WType WT>
-__device__ __forceinline__ float drow_dot(const DRow<WT>& r, const float* x, int lane) {
+__device__ __forceinline__ float down_dot(Smem<WT>& sm, Cons& cs, const float* x, int wave, int lane, unsigned* err) {
     using F = Fmt<WT>;
-    float s = 0.f;
+    using C = RingCfg<WT>;
+    constexpr int G = 4;
+    static_assert(C::LPR8 % G == 0, "down lines");
+    float s = 0.f, rs = 1.f;
 #pragma unroll
-    for (int k = 0; k < DRow<WT>::DCH; ++k) {
-        if (k % 4 == 0) __builtin_amdgcn_sched_barrier(0);
-        const float* xc = x + (k * kWave + lane) * F::CPC;
-        float t = chunk_dot<WT>(r.w[k], xc);
-        if constexpr (WT != WType::BF16) {
-            float cs = 0.f;
+    for (int c0 = 0; c0 < C::LPR8; c0 += G) {
+        ring_wait(cs.k + G, cs.cfull, &sm.full[wave], err);
+        u32x4 w[G];
+        float sc[G];
 #pragma unroll
-            for (int j = 0; j < F::CPC; ++j) cs += xc[j];
-            t -= kBias<WT> * cs;
+        for (int g = 0; g < G; ++g) {
+            w[g] = sm.ring[wave][(cs.k + g) % C::S][lane];
+            if constexpr (C::kQuant) sc[g] = sm.side[wave][(cs.k + g) % C::S][lane];
         }
-        if constexpr (WT == WType::INT4) t *= r.s[k];
-        s += t;
+        // Opaque per group, so the LDS reads of x are not hoisted out of the row loop (the same
+        // inputs serve every row of the wave: hoisted, they would pin LPR8 * CPC registers).
+        int xo = lane;
+        asm volatile("" : "+v"(xo));
+        const f32x4* xq = reinterpret_cast<const f32x4*>(x);
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            float xc[F::CPC];
+#pragma unroll
+            for (int q = 0; q < F::CPC / 4; ++q) {
+                const f32x4 t4 = xq[((c0 + g) * (F::CPC / 4) + q) * kWave + xo];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) xc[4 * q + e] = t4[e];
+            }
+            float t = chunk_dot<WT>(w[g], xc);
+            if constexpr (C::kQuant) {
+                float xs = 0.f;
+#pragma unroll
+                for (int j = 0; j < F::CPC; ++j) xs += xc[j];
+                t -= kBias<WT> * xs;
+            }
+            if constexpr (WT == WType::INT4) t *= sc[g];
+            s += t;
+        }
+        if constexpr (WT == WType::INT8) rs = sc[0];
+        cs.k += G;
+        release(sm, cs, wave, lane);
     }
     s = wave_sum(s);
-    if constexpr (WT == WType::INT8) s *= r.s[0];
+    if constexpr (WT == WType::INT8) s *= rs;
     return s;
 }
 
@@ -236,7 +542,7 @@ __device__ __forceinline__ float embed(const void* w, const void* s, int tok, in
 
 // Phase-end timestamp of this workgroup (thread 0), when stamping is enabled.
 __device__ __forceinline__ void stamp(const DecodeParams& p, int slot) {
-    if (p.stamps && threadIdx.x == 0) p.stamps[blockIdx.x * kStampSlots + slot] = __builtin_amdgcn_s_memrealtime();
+    if (p.stamps && threadIdx.x == 0) *glob(p.stamps + blockIdx.x * kStampSlots + slot) = __builtin_amdgcn_s_memrealtime();
 }
 // In-phase timestamp, recorded for layer 1 only (slots kInPhase + 2 * phase + {0: input arrived, 1: prologue done}).
 constexpr int kInPhase = 100;
@@ -278,42 +584,40 @@ __device__ __forceinline__ void wave_argmax(float& v, int& i) {
     i = bi;
 }
 
+constexpr int kDppRor8 = 0x128;  // row_ror:8: lane i reads lane (i + 8) mod 16 of its 16-lane row
+
+// ---- the kernel ------------------------------------------------------------------------------
+
 template <WType WT>
 __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
     using F = Fmt<WT>;
     constexpr int NX = F::CPL * F::CPC;
-    // LDS: layer input, post-attention residual, this step's RoPE cos/sin, and one 36 KiB region
-    // that holds either the attention tiles, the attention output or the SwiGLU output.
-    __shared__ float xin[H];
-    __shared__ float xa[H];
-    __shared__ __align__(16) float big[9216];
-    __shared__ float rope_c[HD / 2], rope_s[HD / 2];
-    __shared__ float scratch[16];
-    __shared__ float red_v[kWaves];
-    __shared__ int red_i[kWaves];
+    __shared__ Smem<WT> sm;
 
-    const int G = gridDim.x, NW = G * kWaves;
+    if (threadIdx.x < kCW) {
+        sm.full[threadIdx.x] = 0;
+        sm.done[threadIdx.x] = 0;
+        sm.bar[threadIdx.x] = 0;
+    }
+    __syncthreads();  // the only workgroup-wide barrier: loaders never join another one
+    {
+        const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
+        if (w >= kCW) {
+            loader<WT>(p, sm, w - kCW, threadIdx.x % kWave);
+            return;
+        }
+    }
+
+    const int G = gridDim.x, NW = G * kCW;
     unsigned* err = p.d_err;
-    const int pos = *p.d_pos;
-    const int tok = min(max(*p.d_token, 0), VOCAB - 1);
-    const unsigned step = *p.d_step;
+    const int pos = *glob(p.d_pos);
+    const int tok = min(max(*glob(p.d_token), 0), VOCAB - 1);
+    const unsigned step = *glob(p.d_step);
     const unsigned base = step * kEpochStride;
     const int ctx = pos + 1;
     const int nsplit = (ctx + kAttnChunk - 1) / kAttnChunk;
     const int NS = p.max_seq / kAttnChunk;
     const size_t layer_cache = static_cast<size_t>(NKV) * p.max_seq * HD;
-
-    stamp(p, 0);
-    for (int j = threadIdx.x; j < H; j += kThreads) xin[j] = embed<WT>(p.emb, p.emb_s, tok, j);
-    if (threadIdx.x < HD / 2) {  // the angles depend only on the position: one sincos per pair per step
-        float sn, cs;
-        sincosf(static_cast<float>(pos) * gload(p.inv_freq + threadIdx.x), &sn, &cs);
-        rope_s[threadIdx.x] = sn;
-        rope_c[threadIdx.x] = cs;
-    }
-    if (p.residuals && blockIdx.x == 0)
-        for (int j = threadIdx.x; j < H; j += kThreads) p.residuals[j] = xin[j];
-    __syncthreads();
 
     // An opaque copy of the thread index, renewed at every phase: without it the compiler computes
     // the per-thread addresses of all phases up front and keeps them live across the whole layer.
@@ -321,14 +625,38 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
     auto renew = [&] {
         tid = threadIdx.x;
         asm volatile("" : "+v"(tid)::"memory");
-        wave = tid / kWave;
+        wave = __builtin_amdgcn_readfirstlane(tid / kWave);
         lane = tid % kWave;
-        gw = blockIdx.x * kWaves + wave;
+        gw = blockIdx.x * kCW + wave;
     };
+    renew();
+    unsigned ep = 0;  // compute-barrier epoch
+    Cons cs;
+
+    stamp(p, 0);
+    {
+        float ss = 0.f;
+        for (int j = tid; j < H; j += kCT) {
+            const float x = embed<WT>(p.emb, p.emb_s, tok, j);
+            sm.xin[j] = x;
+            ss += x * x;
+        }
+        ss = wave_sum(ss);
+        if (lane == 0) sm.part[wave] = ss;
+    }
+    if (tid < HD / 2) {  // the angles depend only on the position: one sincos per pair per step
+        float sn, csn;
+        sincosf(static_cast<float>(pos) * gload(p.inv_freq + tid), &sn, &csn);
+        sm.rope_s[tid] = sn;
+        sm.rope_c[tid] = csn;
+    }
+    cbar(sm.bar, ep, wave, lane, err);
+    if (p.residuals && blockIdx.x == 0)
+        for (int j = tid; j < H; j += kCT) *glob(p.residuals + j) = sm.xin[j];
 
 #pragma unroll 1
     for (int l = 0; l < NL; ++l) {
-        const DecodeLayer Lw = p.layers[l];
+        const DecodeLayer Lw = load_layer(p.layers, l);
         const unsigned tg = base + l * kTagStride;
         uint64_t* tqkv = p.tqkv + static_cast<size_t>(l) * QKV;
         uint64_t* tatt = p.tatt + static_cast<size_t>(l) * H;
@@ -340,56 +668,41 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
         // ---- qkv (+ attn_norm prologue, RoPE, fp16 KV write); unit = RoPE pair (i, i+32) of a head ----
         renew();
         {
-            Row<WT> ra[kQkvU], rb[kQkvU];
-#pragma unroll
-            for (int i = 0; i < kQkvU; ++i) {
-                const int u = gw + i * NW;
-                if (u < kPairs) {
-                    const int r0 = (u / 32) * HD + u % 32;
-                    load_row<WT>(Lw.wqkv, Lw.sqkv, r0, lane, ra[i]);
-                    load_row<WT>(Lw.wqkv, Lw.sqkv, r0 + 32, lane, rb[i]);
-                }
+            NormW<WT> nw;
+            load_norm<WT>(Lw.attn_norm, lane, nw);
+            if (l > 0) {
+                fetch<H, true>(p.tx + static_cast<size_t>(l) * H, tg - kTagStride + T_X, sm.xin, sm.part, err, tid);
+                cbar(sm.bar, ep, wave, lane, err);
             }
-            if (l > 0) fetch<H>(p.tx + static_cast<size_t>(l) * H, tg - kTagStride + T_X, xin, err, tid);
             stamp_in(p, l, 0, 0);
-            const float inv = rms_inv(xin, p.eps, scratch, tid);
+            const float inv = rms_inv(sm.part, p.eps);
             float xr[NX], xsum;
-            lane_inputs<WT, true>(xin, Lw.attn_norm, inv, xr, xsum, lane);
+            lane_inputs<WT, true>(sm.xin, &nw, inv, xr, xsum, lane);
             stamp_in(p, l, 0, 1);
-            auto finish = [&](int u, float d0, float d1) {
-                const int h = u / 32, i = u % 32, r0 = h * HD + i;
-                float o0 = d0, o1 = d1;
-                if (h < NH + NKV) {
-                    o0 = d0 * rope_c[i] - d1 * rope_s[i];
-                    o1 = d1 * rope_c[i] + d0 * rope_s[i];
-                }
-                tstore(tqkv + r0, o0, tg + T_QKV);
-                tstore(tqkv + r0 + 32, o1, tg + T_QKV);
-                if (h >= NH) {
-                    uint16_t* cache = h < NH + NKV ? p.k_cache : p.v_cache;
-                    const size_t off = l * layer_cache + (static_cast<size_t>((h - NH) % NKV) * p.max_seq + pos) * HD;
-                    cache[off + i] = float_to_half_bits(o0);
-                    cache[off + i + 32] = float_to_half_bits(o1);
-                }
-            };
-#pragma unroll
-            for (int i = 0; i < kQkvU; ++i) {
-                const int u = gw + i * NW;
-                __builtin_amdgcn_sched_barrier(0);
-                if (u < kPairs) {
-                    const float d0 = row_dot<WT>(ra[i], xr, xsum);
-                    const float d1 = row_dot<WT>(rb[i], xr, xsum);
-                    if (lane == 0) finish(u, d0, d1);
-                }
-            }
 #pragma unroll 1
-            for (int u = gw + kQkvU * NW; u < kPairs; u += NW) {  // grids below 256 workgroups
-                const int r0 = (u / 32) * HD + u % 32;
-                load_row<WT>(Lw.wqkv, Lw.sqkv, r0, lane, ra[0]);
-                load_row<WT>(Lw.wqkv, Lw.sqkv, r0 + 32, lane, rb[0]);
-                const float d0 = row_dot<WT>(ra[0], xr, xsum);
-                const float d1 = row_dot<WT>(rb[0], xr, xsum);
-                if (lane == 0) finish(u, d0, d1);
+            for (int u = gw; u < kPairs; u += NW) {
+                Row<WT> ra, rb;
+                take_row<WT>(sm, cs, wave, lane, err, ra);
+                take_row<WT>(sm, cs, wave, lane, err, rb);
+                const float d0 = row_dot<WT>(ra, xr, xsum);
+                const float d1 = row_dot<WT>(rb, xr, xsum);
+                release(sm, cs, wave, lane);
+                if (lane == 0) {
+                    const int h = u / 32, i = u % 32, r0 = h * HD + i;
+                    float o0 = d0, o1 = d1;
+                    if (h < NH + NKV) {
+                        o0 = d0 * sm.rope_c[i] - d1 * sm.rope_s[i];
+                        o1 = d1 * sm.rope_c[i] + d0 * sm.rope_s[i];
+                    }
+                    tstore(tqkv + r0, o0, tg + T_QKV);
+                    tstore(tqkv + r0 + 32, o1, tg + T_QKV);
+                    if (h >= NH) {
+                        uint16_t* cache = h < NH + NKV ? p.k_cache : p.v_cache;
+                        const size_t off = l * layer_cache + (static_cast<size_t>((h - NH) % NKV) * p.max_seq + pos) * HD;
+                        *glob(cache + off + i) = float_to_half_bits(o0);
+                        *glob(cache + off + i + 32) = float_to_half_bits(o1);
+                    }
+                }
             }
         }
         stamp(p, 1 + 6 * l + 0);
@@ -397,12 +710,12 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
         // ---- split-K attention: task = (kv head, 128-token split), one workgroup per task ----
         renew();
         {
-            uint32_t* Ks = reinterpret_cast<uint32_t*>(big);  // [128][33]
-            u32x4* Vs = reinterpret_cast<u32x4*>(big + 4224);  // [128][8]
-            float* ps = big + 8320;                            // [4][128]
-            float* qs = big + 8832;                            // [4][64]
-            float* kvc = big + 9088;                           // [2][64] this token's k, v
-            constexpr int kTile = kAttnChunk * 8 / kThreads;   // 16-byte chunks per thread
+            uint32_t* Ks = reinterpret_cast<uint32_t*>(sm.big);  // [128][33]
+            u32x4* Vs = reinterpret_cast<u32x4*>(sm.big + 4224);  // [128][8]
+            float* ps = sm.big + 8320;                            // [4][128]
+            float* qs = sm.big + 8832;                            // [4][64]
+            float* kvc = sm.big + 9088;                           // [2][64] this token's k, v
+            constexpr int kTile = kAttnChunk * 8 / kCT;           // 16-byte chunks per thread
             const int T = NKV * nsplit;
 #pragma unroll 1
             for (int t = blockIdx.x; t < T; t += G) {
@@ -414,7 +727,7 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
                 u32x4 kt[kTile], vt[kTile];
 #pragma unroll
                 for (int k = 0; k < kTile; ++k) {
-                    const int idx = tid + k * kThreads, r = idx / 8, c = idx % 8;
+                    const int idx = tid + k * kCT, r = idx / 8, c = idx % 8;
                     if (r < n && t0 + r < pos) {
                         kt[k] = load_stream(Kg + static_cast<size_t>(t0 + r) * HD + c * 8);
                         vt[k] = load_stream(Vg + static_cast<size_t>(t0 + r) * HD + c * 8);
@@ -424,11 +737,11 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
                 qs[tid] = wait1(tqkv + (kvh * 4) * HD + tid, tg + T_QKV, err);
                 if (tid < 2 * HD && t0 + n - 1 == pos)
                     kvc[tid] = wait1(tqkv + (tid < HD ? NH * HD : (NH + NKV) * HD - HD) + kvh * HD + tid, tg + T_QKV, err);
-                __syncthreads();
+                cbar(sm.bar, ep, wave, lane, err);
                 if (t == static_cast<int>(blockIdx.x)) stamp_in(p, l, 1, 0);
 #pragma unroll
                 for (int k = 0; k < kTile; ++k) {
-                    const int idx = tid + k * kThreads, r = idx / 8, c = idx % 8;
+                    const int idx = tid + k * kCT, r = idx / 8, c = idx % 8;
                     if (r < n) {
                         u32x4 kv = kt[k], vv = vt[k];
                         if (t0 + r == pos) {  // rounded to fp16 exactly as the qkv phase wrote the cache
@@ -445,7 +758,7 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
                         Vs[r * 8 + c] = vv;
                     }
                 }
-                __syncthreads();
+                cbar(sm.bar, ep, wave, lane, err);
                 // wave w = query head kvh*4 + w; lane scores tokens lane and lane + 64.
                 float s[2];
 #pragma unroll
@@ -470,22 +783,48 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
                 const float lsum = wave_sum(p0 + p1);
                 ps[wave * kAttnChunk + lane] = p0;
                 ps[wave * kAttnChunk + lane + kWave] = p1;
-                __syncthreads();
-                const uint16_t* vrow = reinterpret_cast<const uint16_t*>(Vs);
-                float o = 0.f;
-                for (int j = 0; j < n; ++j) o = fmaf(ps[wave * kAttnChunk + j], half_bits_to_float(vrow[j * HD + lane]), o);
-                const int h = kvh * 4 + wave;
-                if (nsplit == 1) {
-                    tstore(tatt + h * HD + lane, o / lsum, tg + T_ATT);
-                } else {
-                    uint64_t* pp = tpart + (static_cast<size_t>(h) * NS + split) * kPartStride;
-                    tstore(pp + lane, o, tg + T_ATT_PART);
-                    if (lane == 0) {
-                        tstore(pp + HD, m, tg + T_ATT_PART);
-                        tstore(pp + HD + 1, lsum, tg + T_ATT_PART);
+                // P.V: lane = (token phase g, 8-column group c) takes tokens g, g+8, ... of columns
+                // 8c..8c+7; the 8 token phases are then summed across lanes.
+                const int g = lane >> 3, c = lane & 7;
+                float o[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) o[e] = 0.f;
+#pragma unroll 4
+                for (int i = 0; i < kAttnChunk / 8; ++i) {
+                    const int j = g + 8 * i;
+                    if (j < n) {
+                        const float pj = ps[wave * kAttnChunk + j];
+                        const u32x4 vv = Vs[j * 8 + c];
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            o[2 * e] = fmaf(pj, half_bits_to_float(static_cast<uint16_t>(vv[e])), o[2 * e]);
+                            o[2 * e + 1] = fmaf(pj, half_bits_to_float(static_cast<uint16_t>(vv[e] >> 16)), o[2 * e + 1]);
+                        }
                     }
                 }
-                __syncthreads();
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    o[e] += dpp<kDppRor8>(o[e]);
+                    o[e] += __shfl_xor(o[e], 16);
+                    o[e] += __shfl_xor(o[e], 32);
+                }
+                const int h = kvh * 4 + wave;
+                if (g == 0) {
+                    if (nsplit == 1) {
+                        const float il = 1.f / lsum;
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) tstore(tatt + h * HD + c * 8 + e, o[e] * il, tg + T_ATT);
+                    } else {
+                        uint64_t* pp = tpart + (static_cast<size_t>(h) * NS + split) * kPartStride;
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) tstore(pp + c * 8 + e, o[e], tg + T_ATT_PART);
+                        if (lane == 0) {
+                            tstore(pp + HD, m, tg + T_ATT_PART);
+                            tstore(pp + HD + 1, lsum, tg + T_ATT_PART);
+                        }
+                    }
+                }
+                cbar(sm.bar, ep, wave, lane, err);  // the tiles are overwritten next
             }
         }
         stamp(p, 1 + 6 * l + 1);
@@ -535,74 +874,43 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
         // ---- wo + residual ----
         renew();
         {
-            Row<WT> rw[kWoU];
-#pragma unroll
-            for (int i = 0; i < kWoU; ++i)
-                if (gw + i * NW < H) load_row<WT>(Lw.wo, Lw.so, gw + i * NW, lane, rw[i]);
-            fetch<H>(tatt, tg + T_ATT, big, err, tid);
+            fetch<H, false>(tatt, tg + T_ATT, sm.big, sm.part, err, tid);
+            cbar(sm.bar, ep, wave, lane, err);
             stamp_in(p, l, 3, 0);
             float xr[NX], xsum;
-            lane_inputs<WT, false>(big, nullptr, 1.f, xr, xsum, lane);
+            lane_inputs<WT, false>(sm.big, nullptr, 1.f, xr, xsum, lane);
             stamp_in(p, l, 3, 1);
-#pragma unroll
-            for (int i = 0; i < kWoU; ++i) {
-                const int r = gw + i * NW;
-                __builtin_amdgcn_sched_barrier(0);
-                if (r < H) {
-                    const float d = row_dot<WT>(rw[i], xr, xsum);
-                    if (lane == 0) tstore(txa + r, xin[r] + d, tg + T_XA);
-                }
-            }
 #pragma unroll 1
-            for (int r = gw + kWoU * NW; r < H; r += NW) {
-                load_row<WT>(Lw.wo, Lw.so, r, lane, rw[0]);
-                const float d = row_dot<WT>(rw[0], xr, xsum);
-                if (lane == 0) tstore(txa + r, xin[r] + d, tg + T_XA);
+            for (int r = gw; r < H; r += NW) {
+                Row<WT> rw;
+                take_row<WT>(sm, cs, wave, lane, err, rw);
+                const float d = row_dot<WT>(rw, xr, xsum);
+                release(sm, cs, wave, lane);
+                if (lane == 0) tstore(txa + r, sm.xin[r] + d, tg + T_XA);
             }
         }
         stamp(p, 1 + 6 * l + 3);
 
         // ---- gate_up (+ ffn_norm prologue, SwiGLU); unit = gate row u and up row u + inter ----
-        // PF units in flight per wave (a ring): each consumed slot is refilled with the unit PF ahead.
         renew();
         {
-            constexpr int PF = WT == WType::BF16 ? 2 : WT == WType::INT8 ? 4 : kGuU;  // 16 KiB per wave
-            Row<WT> rg[PF], ru[PF];
-#pragma unroll
-            for (int i = 0; i < PF; ++i) {
-                const int u = gw + i * NW;
-                if (u < INTER) {
-                    load_row<WT>(Lw.wgu, Lw.sgu, u, lane, rg[i]);
-                    load_row<WT>(Lw.wgu, Lw.sgu, u + INTER, lane, ru[i]);
-                }
-            }
-            fetch<H>(txa, tg + T_XA, xa, err, tid);
+            NormW<WT> nw;
+            load_norm<WT>(Lw.ffn_norm, lane, nw);
+            fetch<H, true>(txa, tg + T_XA, sm.xa, sm.part, err, tid);
+            cbar(sm.bar, ep, wave, lane, err);
             stamp_in(p, l, 4, 0);
-            const float inv = rms_inv(xa, p.eps, scratch, tid);
+            const float inv = rms_inv(sm.part, p.eps);
             float xr[NX], xsum;
-            lane_inputs<WT, true>(xa, Lw.ffn_norm, inv, xr, xsum, lane);
+            lane_inputs<WT, true>(sm.xa, &nw, inv, xr, xsum, lane);
             stamp_in(p, l, 4, 1);
-#pragma unroll
-            for (int i = 0; i < kGuU; ++i) {
-                const int u = gw + i * NW;
-                __builtin_amdgcn_sched_barrier(0);
-                if (u < INTER) {
-                    const float gv = row_dot<WT>(rg[i % PF], xr, xsum);
-                    const float uv = row_dot<WT>(ru[i % PF], xr, xsum);
-                    if (lane == 0) tstore(tact + u, silu(gv) * uv, tg + T_ACT);
-                }
-                const int un = gw + (i + PF) * NW;
-                if (i + PF < kGuU && un < INTER) {
-                    load_row<WT>(Lw.wgu, Lw.sgu, un, lane, rg[i % PF]);
-                    load_row<WT>(Lw.wgu, Lw.sgu, un + INTER, lane, ru[i % PF]);
-                }
-            }
 #pragma unroll 1
-            for (int u = gw + kGuU * NW; u < INTER; u += NW) {
-                load_row<WT>(Lw.wgu, Lw.sgu, u, lane, rg[0]);
-                load_row<WT>(Lw.wgu, Lw.sgu, u + INTER, lane, ru[0]);
-                const float gv = row_dot<WT>(rg[0], xr, xsum);
-                const float uv = row_dot<WT>(ru[0], xr, xsum);
+            for (int u = gw; u < INTER; u += NW) {
+                Row<WT> rg, ru;
+                take_row<WT>(sm, cs, wave, lane, err, rg);
+                take_row<WT>(sm, cs, wave, lane, err, ru);
+                const float gv = row_dot<WT>(rg, xr, xsum);
+                const float uv = row_dot<WT>(ru, xr, xsum);
+                release(sm, cs, wave, lane);
                 if (lane == 0) tstore(tact + u, silu(gv) * uv, tg + T_ACT);
             }
         }
@@ -611,89 +919,68 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
         // ---- down + residual (8192-wide rows, inputs read from LDS) ----
         renew();
         {
-            constexpr int PD = WT == WType::BF16 ? 1 : kDownU;  // rows in flight (16 KiB per wave for bf16)
-            DRow<WT> rd[PD];
-#pragma unroll
-            for (int i = 0; i < PD; ++i)
-                if (gw + i * NW < H) load_drow<WT>(Lw.wd, Lw.sd, gw + i * NW, lane, rd[i]);
-            fetch<INTER>(tact, tg + T_ACT, big, err, tid);
+            fetch<INTER, false, F::CPC>(tact, tg + T_ACT, sm.big, sm.part, err, tid);
+            cbar(sm.bar, ep, wave, lane, err);
             stamp_in(p, l, 5, 0);
-            auto finish = [&](int r, float d) {
-                const float xn = xa[r] + d;
-                tstore(txo + r, xn, tg + T_X);
-                if (p.residuals) p.residuals[static_cast<size_t>(l + 1) * H + r] = xn;
-            };
-#pragma unroll
-            for (int i = 0; i < PD; ++i) {
-                const int r = gw + i * NW;
-                if (r < H) {
-                    const float d = drow_dot<WT>(rd[i], big, lane);
-                    if (lane == 0) finish(r, d);
+#pragma unroll 1
+            for (int r = gw; r < H; r += NW) {
+                const float d = down_dot<WT>(sm, cs, sm.big, wave, lane, err);
+                if (lane == 0) {
+                    const float xn = sm.xa[r] + d;
+                    tstore(txo + r, xn, tg + T_X);
+                    if (p.residuals) *glob(p.residuals + static_cast<size_t>(l + 1) * H + r) = xn;
                 }
             }
-#pragma unroll 1
-            for (int r = gw + PD * NW; r < H; r += NW) {
-                load_drow<WT>(Lw.wd, Lw.sd, r, lane, rd[0]);
-                const float d = drow_dot<WT>(rd[0], big, lane);
-                if (lane == 0) finish(r, d);
-            }
-            __syncthreads();  // `big` is reused by the next layer's attention tiles
         }
         stamp(p, 1 + 6 * l + 5);
     }
 
-    // ---- lm_head (+ final norm) with the argmax folded in; R rows per wave per step, double-buffered ----
+    // ---- lm_head (+ final norm) with the argmax folded in; unit = kLmR consecutive rows ----
     renew();
     {
-        constexpr int R = 2;
-        Row<WT> cur[R], nxt[R];
-        const int step_rows = NW * R;
-        int r0 = gw * R;
-#pragma unroll
-        for (int i = 0; i < R; ++i)
-            if (r0 + i < VOCAB) load_row<WT>(p.emb, p.emb_s, r0 + i, lane, cur[i]);
-        fetch<H>(p.tx + static_cast<size_t>(NL) * H, base + (NL - 1) * kTagStride + T_X, xin, err, tid);
-        const float inv = rms_inv(xin, p.eps, scratch, tid);
+        NormW<WT> nw;
+        load_norm<WT>(p.final_norm, lane, nw);
+        fetch<H, true>(p.tx + static_cast<size_t>(NL) * H, base + (NL - 1) * kTagStride + T_X, sm.xin, sm.part, err, tid);
+        cbar(sm.bar, ep, wave, lane, err);
+        const float inv = rms_inv(sm.part, p.eps);
         float xr[NX], xsum;
-        lane_inputs<WT, true>(xin, p.final_norm, inv, xr, xsum, lane);
+        lane_inputs<WT, true>(sm.xin, &nw, inv, xr, xsum, lane);
         float bv = -INFINITY;
         int bi = 0x7fffffff;
 #pragma unroll 1
-        for (; r0 < VOCAB; r0 += step_rows) {
-            const int rn = r0 + step_rows;
+        for (int u = gw; u < VOCAB / kLmR; u += NW) {
+            Row<WT> rr[kLmR];
 #pragma unroll
-            for (int i = 0; i < R; ++i)
-                if (rn + i < VOCAB) load_row<WT>(p.emb, p.emb_s, rn + i, lane, nxt[i]);
+            for (int i = 0; i < kLmR; ++i) take_row<WT>(sm, cs, wave, lane, err, rr[i]);
+            float d[kLmR];
 #pragma unroll
-            for (int i = 0; i < R; ++i) {
-                const int r = r0 + i;
-                if (r < VOCAB) {
-                    const float d = row_dot<WT>(cur[i], xr, xsum);
-                    if (lane == 0) p.logits[r] = d;
-                    if (arg_better(d, r, bv, bi)) {
-                        bv = d;
-                        bi = r;
-                    }
+            for (int i = 0; i < kLmR; ++i) d[i] = row_dot<WT>(rr[i], xr, xsum);
+            release(sm, cs, wave, lane);
+#pragma unroll
+            for (int i = 0; i < kLmR; ++i) {
+                const int r = u * kLmR + i;
+                if (lane == 0) *glob(p.logits + r) = d[i];
+                if (arg_better(d[i], r, bv, bi)) {
+                    bv = d[i];
+                    bi = r;
                 }
             }
-#pragma unroll
-            for (int i = 0; i < R; ++i) cur[i] = nxt[i];
         }
         if (lane == 0) {
-            red_v[wave] = bv;
-            red_i[wave] = bi;
+            sm.red_v[wave] = bv;
+            sm.red_i[wave] = bi;
         }
-        __syncthreads();
+        cbar(sm.bar, ep, wave, lane, err);
         if (tid == 0) {
-            for (int w = 1; w < kWaves; ++w)
-                if (arg_better(red_v[w], red_i[w], bv, bi)) {
-                    bv = red_v[w];
-                    bi = red_i[w];
+            for (int w = 1; w < kCW; ++w)
+                if (arg_better(sm.red_v[w], sm.red_i[w], bv, bi)) {
+                    bv = sm.red_v[w];
+                    bi = sm.red_i[w];
                 }
             tstore(p.targ + 2 * blockIdx.x, bv, base + T_ARG);
             tstore(p.targ + 2 * blockIdx.x + 1, __builtin_bit_cast(float, bi), base + T_ARG);
         }
-        __syncthreads();
+        cbar(sm.bar, ep, wave, lane, err);  // red_* are reused below
     }
     stamp(p, 97);
 
@@ -701,7 +988,7 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
     if (blockIdx.x == 0) {
         float v = -INFINITY;
         int i = 0x7fffffff;
-        for (int g = tid; g < G; g += kThreads) {
+        for (int g = tid; g < G; g += kCT) {
             const float gv = wait1(p.targ + 2 * g, base + T_ARG, err);
             const int gi = __builtin_bit_cast(int, wait1(p.targ + 2 * g + 1, base + T_ARG, err));
             if (arg_better(gv, gi, v, i)) {
@@ -711,19 +998,19 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
         }
         wave_argmax(v, i);
         if (lane == 0) {
-            red_v[wave] = v;
-            red_i[wave] = i;
+            sm.red_v[wave] = v;
+            sm.red_i[wave] = i;
         }
-        __syncthreads();
+        cbar(sm.bar, ep, wave, lane, err);
         if (tid == 0) {
-            for (int w = 1; w < kWaves; ++w)
-                if (arg_better(red_v[w], red_i[w], v, i)) {
-                    v = red_v[w];
-                    i = red_i[w];
+            for (int w = 1; w < kCW; ++w)
+                if (arg_better(sm.red_v[w], sm.red_i[w], v, i)) {
+                    v = sm.red_v[w];
+                    i = sm.red_i[w];
                 }
-            *p.d_token = min(max(i, 0), VOCAB - 1);
-            *p.d_pos = pos + 1;
-            *p.d_step = step + 1;
+            *glob(p.d_token) = min(max(i, 0), VOCAB - 1);
+            *glob(p.d_pos) = pos + 1;
+            *glob(p.d_step) = step + 1;
         }
         stamp(p, 98);
     }
