@@ -472,10 +472,35 @@ __device__ __forceinline__ float row_dot(const Row<WT>& r, const float* xr, floa
     return s;
 }
 
+// Per-chunk sums of the lane's down-projection inputs (the bias correction of quantised chunks);
+// the same for every row, so computed once per phase.
+template <WType WT>
+struct DownSums {
+    float v[RingCfg<WT>::kQuant ? RingCfg<WT>::LPR8 : 1];
+};
+template <WType WT>
+__device__ __forceinline__ void down_sums(const float* x, int lane, DownSums<WT>& ds) {
+    using F = Fmt<WT>;
+    if constexpr (RingCfg<WT>::kQuant) {
+        const f32x4* xq = reinterpret_cast<const f32x4*>(x);
+#pragma unroll
+        for (int c = 0; c < RingCfg<WT>::LPR8; ++c) {
+            float t = 0.f;
+#pragma unroll
+            for (int q = 0; q < F::CPC / 4; ++q) {
+                const f32x4 t4 = xq[(c * (F::CPC / 4) + q) * kWave + lane];
+                t += (t4[0] + t4[1]) + (t4[2] + t4[3]);
+            }
+            ds.v[c] = t;
+        }
+    }
+}
+
 // Dot of one 8192-wide row (down projection) taken from the ring four lines at a time, inputs from
 // LDS in the swz layout.
 template <WType WT>
-__device__ __forceinline__ float down_dot(Smem<WT>& sm, Cons& cs, const float* x, int wave, int lane, unsigned* err) {
+__device__ __forceinline__ float down_dot(Smem<WT>& sm, Cons& cs, const float* x, const DownSums<WT>& ds, int wave,
+                                          int lane, unsigned* err) {
     using F = Fmt<WT>;
     using C = RingCfg<WT>;
     constexpr int G = 4;
@@ -506,12 +531,7 @@ __device__ __forceinline__ float down_dot(Smem<WT>& sm, Cons& cs, const float* x
                 for (int e = 0; e < 4; ++e) xc[4 * q + e] = t4[e];
             }
             float t = chunk_dot<WT>(w[g], xc);
-            if constexpr (C::kQuant) {
-                float xs = 0.f;
-#pragma unroll
-                for (int j = 0; j < F::CPC; ++j) xs += xc[j];
-                t -= kBias<WT> * xs;
-            }
+            if constexpr (C::kQuant) t -= kBias<WT> * ds.v[c0 + g];
             if constexpr (WT == WType::INT4) t *= sc[g];
             s += t;
         }
@@ -922,9 +942,11 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
             fetch<INTER, false, F::CPC>(tact, tg + T_ACT, sm.big, sm.part, err, tid);
             cbar(sm.bar, ep, wave, lane, err);
             stamp_in(p, l, 5, 0);
+            DownSums<WT> dsum;
+            down_sums<WT>(sm.big, lane, dsum);
 #pragma unroll 1
             for (int r = gw; r < H; r += NW) {
-                const float d = down_dot<WT>(sm, cs, sm.big, wave, lane, err);
+                const float d = down_dot<WT>(sm, cs, sm.big, dsum, wave, lane, err);
                 if (lane == 0) {
                     const float xn = sm.xa[r] + d;
                     tstore(txo + r, xn, tg + T_X);

@@ -57,8 +57,11 @@ __device__ __forceinline__ float chunk_dot(const u32x4 v, const float* x) {
     } else {
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-            const uint32_t lo = v[t] & 0x0F0F0F0Fu;
-            const uint32_t hi = (v[t] >> 4) & 0x0F0F0F0Fu;
+            uint32_t lo = v[t] & 0x0F0F0F0Fu;
+            uint32_t hi = (v[t] >> 4) & 0x0F0F0F0Fu;
+            // Opaque to the optimiser: with the masked words kept whole, each nibble converts straight
+            // from its byte (v_cvt_f32_ubyteN) instead of a bit-field extract plus a conversion.
+            asm("" : "+v"(lo), "+v"(hi));
 #pragma unroll
             for (int b = 0; b < 4; ++b) {
                 acc = fmaf(static_cast<float>((lo >> (8 * b)) & 0xffu), x[8 * t + 2 * b], acc);

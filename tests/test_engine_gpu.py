@@ -210,3 +210,37 @@ def test_sequence_full_and_token_range(model_path):
         assert eng.pos == 0
         nxt, lg = eng.step(5, want_logits=True)
         assert eng.pos == 1 and nxt == int(np.argmax(lg))
+
+
+@pytest.mark.parametrize("wd", ["int4", "bf16"])
+def test_persistent_long_context_matches_multikernel(wd, model_path, monkeypatch):
+    """Contexts past one 128-token chunk: the persistent kernel's split-K attention and its LSE merge
+    (up to 6 splits here) against the multi-kernel path, whose split-K attention kernels are checked
+    against the float64 oracle up to context 8192 in test_kernels_gpu.py.  Both engines are
+    teacher-forced with the same tokens to context 700."""
+    steps = 700
+    monkeypatch.setenv("CUDALLM_PERSISTENT", "0")
+    ref = E.Engine(model_path(wd), max_seq_len=1024)
+    monkeypatch.delenv("CUDALLM_PERSISTENT")
+    eng = E.Engine(model_path(wd), max_seq_len=1024)
+    try:
+        toks = [128000]
+        worst, agree, checked = 0.0, 0, 0
+        for i in range(steps):
+            check = i % 25 == 24 or i in (127, 128, 129, 511, 512, 513)
+            n_ref, lg_ref = ref.step(toks[-1], want_logits=check)
+            n_eng, lg_eng = eng.step(toks[-1], want_logits=check)
+            if check:
+                scale = float(np.abs(lg_ref).max())
+                worst = max(worst, float(np.abs(lg_eng - lg_ref).max()) / scale)
+                agree += int(n_eng == n_ref)
+                checked += 1
+            toks.append(n_ref)
+        print(f"[engine] {wd} persistent vs multi-kernel to ctx {steps}: worst rel logit diff {worst:.2e}, "
+              f"argmax agree {agree}/{checked}", flush=True)
+        assert worst < 2e-3
+        assert agree >= checked - 1
+        assert eng.pos == ref.pos == steps
+    finally:
+        eng.close()
+        ref.close()
