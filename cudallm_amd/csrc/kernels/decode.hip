@@ -47,7 +47,8 @@ static_assert(kThreads == 2 * kCT, "one loader wave per compute wave");
 constexpr int H = 2048, INTER = 8192, NH = 32, NKV = 8, HD = 64, QKV = (NH + 2 * NKV) * HD, VOCAB = 128256, NL = 16;
 constexpr int kTagStride = 8;            // tag slots per layer
 constexpr unsigned kEpochStride = 256;   // tag slots per step
-constexpr unsigned kSpinCap = 1u << 20;  // bounded waits (~1 s of polling)
+constexpr unsigned kSpinCap = 1u << 20;     // bounded waits on other workgroups (~1 s of polling)
+constexpr unsigned kLdsSpinCap = 1u << 26;  // bounded waits inside the workgroup (~2 s)
 constexpr int kPartStride = HD + 2;      // o[64], m, l
 constexpr int kPairs = QKV / 2;          // RoPE pairs (i, i+32) of every q/k/v head
 constexpr int kLmR = 2;                  // lm_head rows per unit
@@ -144,30 +145,55 @@ __device__ __forceinline__ float wait1(const uint64_t* a, unsigned tag, unsigned
 
 // ---- workgroup-local synchronisation (LDS) ---------------------------------------------------
 
-__device__ __forceinline__ int lds_load(int* a) { return __hip_atomic_load(a, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP); }
-__device__ __forceinline__ void lds_store(int* a, int v) { __hip_atomic_store(a, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP); }
+// The flags below only order LDS accesses, and the LDS executes a wave's accesses in issue order,
+// so a relaxed access behind a compiler barrier is enough.  A release/acquire atomic would also wait
+// for the wave's outstanding global stores (one counter covers loads and stores on this GPU): a full
+// memory round trip per ring slot or barrier.
+__device__ __forceinline__ int lds_load(int* a) {
+    const int v = __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    asm volatile("" ::: "memory");  // later LDS reads stay after this one
+    return v;
+}
+__device__ __forceinline__ void lds_store(int* a, int v) {
+    asm volatile("" ::: "memory");  // earlier LDS accesses stay before this one
+    __hip_atomic_store(a, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// One step of a bounded wait on a partner in this workgroup.  No global access on this path (it
+// would make every wait end with a full drain of the wave's memory counter); an overrun is kept
+// in `lbad` and reported once, when the wave finishes.
+__device__ __forceinline__ bool lds_give_up(unsigned& spins, bool& lbad) {
+    if (++spins >= kLdsSpinCap) {
+        lbad = true;
+        return true;
+    }
+    __builtin_amdgcn_s_sleep(1);
+    return false;
+}
 
 // Barrier of the kCW compute waves: each publishes its epoch, then waits for all.  Orders the
 // LDS writes made before it against the reads made after it.
-__device__ __forceinline__ void cbar(unsigned* bar, unsigned& ep, int wave, int lane, unsigned* err) {
+__device__ __forceinline__ void cbar(unsigned* bar, unsigned& ep, int wave, int lane, bool& lbad) {
     ++ep;
-    if (lane == 0) __hip_atomic_store(bar + wave, ep, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+    asm volatile("" ::: "memory");
+    if (lane == 0) __hip_atomic_store(bar + wave, ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     unsigned spins = 0;
     for (;;) {
         unsigned lo = ~0u;
 #pragma unroll
-        for (int w = 0; w < kCW; ++w) lo = min(lo, __hip_atomic_load(bar + w, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP));
-        if (lo >= ep || give_up(spins, err)) break;
+        for (int w = 0; w < kCW; ++w) lo = min(lo, __hip_atomic_load(bar + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+        if (lo >= ep || lds_give_up(spins, lbad)) break;
     }
+    asm volatile("" ::: "memory");
 }
 
 // Wait until the loader has published `need` lines of this wave's ring.
-__device__ __forceinline__ void ring_wait(int need, int& cfull, int* full, unsigned* err) {
+__device__ __forceinline__ void ring_wait(int need, int& cfull, int* full, bool& lbad) {
     if (cfull >= need) return;
     unsigned spins = 0;
     for (;;) {
         cfull = lds_load(full);
-        if (cfull >= need || give_up(spins, err)) break;
+        if (cfull >= need || lds_give_up(spins, lbad)) break;
     }
 }
 
@@ -310,6 +336,7 @@ __device__ void loader(const DecodeParams& p, Smem<WT>& sm, int wave, int lane) 
 #pragma unroll
     for (int s = 0; s < kNB; ++s) issue(s);
     int k = 0, cdone = 0;
+    bool lbad = false;
     for (;;) {
         bool any = false;
 #pragma unroll
@@ -320,7 +347,7 @@ __device__ void loader(const DecodeParams& p, Smem<WT>& sm, int wave, int lane) 
                     unsigned spins = 0;
                     for (;;) {
                         cdone = lds_load(&sm.done[wave]);
-                        if (k - cdone < C::S || give_up(spins, err)) break;
+                        if (k - cdone < C::S || lds_give_up(spins, lbad)) break;
                     }
                 }
                 const int slot = k % C::S;
@@ -334,6 +361,7 @@ __device__ void loader(const DecodeParams& p, Smem<WT>& sm, int wave, int lane) 
         if (!st.have && !st.end) st.next_seg();
         if (!any && st.end) break;
     }
+    if (lbad) fail(err);
 }
 
 // ---- compute-wave helpers --------------------------------------------------------------------
@@ -445,9 +473,9 @@ struct Cons {
 };
 
 template <WType WT>
-__device__ __forceinline__ void take_row(Smem<WT>& sm, Cons& cs, int wave, int lane, unsigned* err, Row<WT>& r) {
+__device__ __forceinline__ void take_row(Smem<WT>& sm, Cons& cs, int wave, int lane, bool& lbad, Row<WT>& r) {
     using C = RingCfg<WT>;
-    ring_wait(cs.k + C::LPR2, cs.cfull, &sm.full[wave], err);
+    ring_wait(cs.k + C::LPR2, cs.cfull, &sm.full[wave], lbad);
 #pragma unroll
     for (int c = 0; c < C::LPR2; ++c) r.w[c] = sm.ring[wave][(cs.k + c) % C::S][lane];
     if constexpr (C::kQuant) r.s = sm.side[wave][cs.k % C::S][lane];
@@ -500,7 +528,7 @@ __device__ __forceinline__ void down_sums(const float* x, int lane, DownSums<WT>
 // LDS in the swz layout.
 template <WType WT>
 __device__ __forceinline__ float down_dot(Smem<WT>& sm, Cons& cs, const float* x, const DownSums<WT>& ds, int wave,
-                                          int lane, unsigned* err) {
+                                          int lane, bool& lbad) {
     using F = Fmt<WT>;
     using C = RingCfg<WT>;
     constexpr int G = 4;
@@ -508,7 +536,7 @@ __device__ __forceinline__ float down_dot(Smem<WT>& sm, Cons& cs, const float* x
     float s = 0.f, rs = 1.f;
 #pragma unroll
     for (int c0 = 0; c0 < C::LPR8; c0 += G) {
-        ring_wait(cs.k + G, cs.cfull, &sm.full[wave], err);
+        ring_wait(cs.k + G, cs.cfull, &sm.full[wave], lbad);
         u32x4 w[G];
         float sc[G];
 #pragma unroll
@@ -569,6 +597,11 @@ constexpr int kInPhase = 100;
 __device__ __forceinline__ void stamp_in(const DecodeParams& p, int l, int phase, int k) {
     if (l == 1) stamp(p, kInPhase + 2 * phase + k);
 }
+
+// Drain this wave's outstanding global accesses before a row loop.  They are long complete by then
+// (earlier phases' stores); without it the compiler, which cannot tell the loop's first iteration
+// from the others, waits for them in every iteration before reusing their registers.
+__device__ __forceinline__ void drain() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 // Argmax order: larger value first, then lower index (numpy's tie rule).  NaN never wins.
 __device__ __forceinline__ bool arg_better(float v, int i, float bv, int bi) { return v > bv || (v == bv && i < bi); }
@@ -650,7 +683,8 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
         gw = blockIdx.x * kCW + wave;
     };
     renew();
-    unsigned ep = 0;  // compute-barrier epoch
+    unsigned ep = 0;     // compute-barrier epoch
+    bool lbad = false;   // an in-workgroup wait overran (reported at the end)
     Cons cs;
 
     stamp(p, 0);
@@ -670,7 +704,7 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
         sm.rope_s[tid] = sn;
         sm.rope_c[tid] = csn;
     }
-    cbar(sm.bar, ep, wave, lane, err);
+    cbar(sm.bar, ep, wave, lane, lbad);
     if (p.residuals && blockIdx.x == 0)
         for (int j = tid; j < H; j += kCT) *glob(p.residuals + j) = sm.xin[j];
 
@@ -692,18 +726,19 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
             load_norm<WT>(Lw.attn_norm, lane, nw);
             if (l > 0) {
                 fetch<H, true>(p.tx + static_cast<size_t>(l) * H, tg - kTagStride + T_X, sm.xin, sm.part, err, tid);
-                cbar(sm.bar, ep, wave, lane, err);
+                cbar(sm.bar, ep, wave, lane, lbad);
             }
             stamp_in(p, l, 0, 0);
             const float inv = rms_inv(sm.part, p.eps);
             float xr[NX], xsum;
             lane_inputs<WT, true>(sm.xin, &nw, inv, xr, xsum, lane);
             stamp_in(p, l, 0, 1);
+            drain();
 #pragma unroll 1
             for (int u = gw; u < kPairs; u += NW) {
                 Row<WT> ra, rb;
-                take_row<WT>(sm, cs, wave, lane, err, ra);
-                take_row<WT>(sm, cs, wave, lane, err, rb);
+                take_row<WT>(sm, cs, wave, lane, lbad, ra);
+                take_row<WT>(sm, cs, wave, lane, lbad, rb);
                 const float d0 = row_dot<WT>(ra, xr, xsum);
                 const float d1 = row_dot<WT>(rb, xr, xsum);
                 release(sm, cs, wave, lane);
@@ -757,7 +792,7 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
                 qs[tid] = wait1(tqkv + (kvh * 4) * HD + tid, tg + T_QKV, err);
                 if (tid < 2 * HD && t0 + n - 1 == pos)
                     kvc[tid] = wait1(tqkv + (tid < HD ? NH * HD : (NH + NKV) * HD - HD) + kvh * HD + tid, tg + T_QKV, err);
-                cbar(sm.bar, ep, wave, lane, err);
+                cbar(sm.bar, ep, wave, lane, lbad);
                 if (t == static_cast<int>(blockIdx.x)) stamp_in(p, l, 1, 0);
 #pragma unroll
                 for (int k = 0; k < kTile; ++k) {
@@ -778,7 +813,7 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
                         Vs[r * 8 + c] = vv;
                     }
                 }
-                cbar(sm.bar, ep, wave, lane, err);
+                cbar(sm.bar, ep, wave, lane, lbad);
                 // wave w = query head kvh*4 + w; lane scores tokens lane and lane + 64.
                 float s[2];
 #pragma unroll
@@ -844,7 +879,7 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
                         }
                     }
                 }
-                cbar(sm.bar, ep, wave, lane, err);  // the tiles are overwritten next
+                cbar(sm.bar, ep, wave, lane, lbad);  // the tiles are overwritten next
             }
         }
         stamp(p, 1 + 6 * l + 1);
@@ -895,15 +930,16 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
         renew();
         {
             fetch<H, false>(tatt, tg + T_ATT, sm.big, sm.part, err, tid);
-            cbar(sm.bar, ep, wave, lane, err);
+            cbar(sm.bar, ep, wave, lane, lbad);
             stamp_in(p, l, 3, 0);
             float xr[NX], xsum;
             lane_inputs<WT, false>(sm.big, nullptr, 1.f, xr, xsum, lane);
             stamp_in(p, l, 3, 1);
+            drain();
 #pragma unroll 1
             for (int r = gw; r < H; r += NW) {
                 Row<WT> rw;
-                take_row<WT>(sm, cs, wave, lane, err, rw);
+                take_row<WT>(sm, cs, wave, lane, lbad, rw);
                 const float d = row_dot<WT>(rw, xr, xsum);
                 release(sm, cs, wave, lane);
                 if (lane == 0) tstore(txa + r, sm.xin[r] + d, tg + T_XA);
@@ -917,17 +953,18 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
             NormW<WT> nw;
             load_norm<WT>(Lw.ffn_norm, lane, nw);
             fetch<H, true>(txa, tg + T_XA, sm.xa, sm.part, err, tid);
-            cbar(sm.bar, ep, wave, lane, err);
+            cbar(sm.bar, ep, wave, lane, lbad);
             stamp_in(p, l, 4, 0);
             const float inv = rms_inv(sm.part, p.eps);
             float xr[NX], xsum;
             lane_inputs<WT, true>(sm.xa, &nw, inv, xr, xsum, lane);
             stamp_in(p, l, 4, 1);
+            drain();
 #pragma unroll 1
             for (int u = gw; u < INTER; u += NW) {
                 Row<WT> rg, ru;
-                take_row<WT>(sm, cs, wave, lane, err, rg);
-                take_row<WT>(sm, cs, wave, lane, err, ru);
+                take_row<WT>(sm, cs, wave, lane, lbad, rg);
+                take_row<WT>(sm, cs, wave, lane, lbad, ru);
                 const float gv = row_dot<WT>(rg, xr, xsum);
                 const float uv = row_dot<WT>(ru, xr, xsum);
                 release(sm, cs, wave, lane);
@@ -940,13 +977,14 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
         renew();
         {
             fetch<INTER, false, F::CPC>(tact, tg + T_ACT, sm.big, sm.part, err, tid);
-            cbar(sm.bar, ep, wave, lane, err);
+            cbar(sm.bar, ep, wave, lane, lbad);
             stamp_in(p, l, 5, 0);
             DownSums<WT> dsum;
             down_sums<WT>(sm.big, lane, dsum);
+            drain();
 #pragma unroll 1
             for (int r = gw; r < H; r += NW) {
-                const float d = down_dot<WT>(sm, cs, sm.big, dsum, wave, lane, err);
+                const float d = down_dot<WT>(sm, cs, sm.big, dsum, wave, lane, lbad);
                 if (lane == 0) {
                     const float xn = sm.xa[r] + d;
                     tstore(txo + r, xn, tg + T_X);
@@ -963,17 +1001,22 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
         NormW<WT> nw;
         load_norm<WT>(p.final_norm, lane, nw);
         fetch<H, true>(p.tx + static_cast<size_t>(NL) * H, base + (NL - 1) * kTagStride + T_X, sm.xin, sm.part, err, tid);
-        cbar(sm.bar, ep, wave, lane, err);
+        cbar(sm.bar, ep, wave, lane, lbad);
         const float inv = rms_inv(sm.part, p.eps);
         float xr[NX], xsum;
         lane_inputs<WT, true>(sm.xin, &nw, inv, xr, xsum, lane);
         float bv = -INFINITY;
         int bi = 0x7fffffff;
+        // Logits are collected across lanes (lane j holds the wave's j-th row) and stored 64 at a time:
+        // a store per row would make every iteration wait for the previous one's store to drain.
+        float lg = 0.f;
+        int lr = 0, nrow = 0;
+        drain();
 #pragma unroll 1
         for (int u = gw; u < VOCAB / kLmR; u += NW) {
             Row<WT> rr[kLmR];
 #pragma unroll
-            for (int i = 0; i < kLmR; ++i) take_row<WT>(sm, cs, wave, lane, err, rr[i]);
+            for (int i = 0; i < kLmR; ++i) take_row<WT>(sm, cs, wave, lane, lbad, rr[i]);
             float d[kLmR];
 #pragma unroll
             for (int i = 0; i < kLmR; ++i) d[i] = row_dot<WT>(rr[i], xr, xsum);
@@ -981,18 +1024,28 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
 #pragma unroll
             for (int i = 0; i < kLmR; ++i) {
                 const int r = u * kLmR + i;
-                if (lane == 0) *glob(p.logits + r) = d[i];
+                if (lane == nrow + i) {
+                    lg = d[i];
+                    lr = r;
+                }
                 if (arg_better(d[i], r, bv, bi)) {
                     bv = d[i];
                     bi = r;
                 }
             }
+            nrow += kLmR;
+            if (nrow == kWave) {  // wave-uniform: a branch, so the drain below runs only here
+                *glob(p.logits + lr) = lg;
+                drain();  // nothing left pending for the hot path
+                nrow = 0;
+            }
         }
+        if (lane < nrow) *glob(p.logits + lr) = lg;
         if (lane == 0) {
             sm.red_v[wave] = bv;
             sm.red_i[wave] = bi;
         }
-        cbar(sm.bar, ep, wave, lane, err);
+        cbar(sm.bar, ep, wave, lane, lbad);
         if (tid == 0) {
             for (int w = 1; w < kCW; ++w)
                 if (arg_better(sm.red_v[w], sm.red_i[w], bv, bi)) {
@@ -1002,7 +1055,7 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
             tstore(p.targ + 2 * blockIdx.x, bv, base + T_ARG);
             tstore(p.targ + 2 * blockIdx.x + 1, __builtin_bit_cast(float, bi), base + T_ARG);
         }
-        cbar(sm.bar, ep, wave, lane, err);  // red_* are reused below
+        cbar(sm.bar, ep, wave, lane, lbad);  // red_* are reused below
     }
     stamp(p, 97);
 
@@ -1023,7 +1076,7 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
             sm.red_v[wave] = v;
             sm.red_i[wave] = i;
         }
-        cbar(sm.bar, ep, wave, lane, err);
+        cbar(sm.bar, ep, wave, lane, lbad);
         if (tid == 0) {
             for (int w = 1; w < kCW; ++w)
                 if (arg_better(sm.red_v[w], sm.red_i[w], v, i)) {
@@ -1036,6 +1089,7 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
         }
         stamp(p, 98);
     }
+    if (lbad) fail(err);
 }
 
 }  // namespace dk
