@@ -14,7 +14,7 @@
 //    step and streams the rows as 1 KiB lines (64 lanes x 16 B) into the compute wave's LDS ring,
 //    running ahead across phase boundaries; it only ever waits for ring space.  HBM therefore
 //    keeps streaming while compute waves wait for the inputs of their next phase.  The loader
-//    keeps kNB lines in flight with ordinary 128-bit loads and copies each landed line into the
+//    keeps RingCfg::NB lines in flight with ordinary 128-bit loads and copies each landed line into the
 //    ring; quantised lines carry one 32-bit side value per lane (row scale or group scale).
 //  * Phases exchange vectors through tagged 64-bit words (see decode.h).  A consumer loads the
 //    vector it needs with relaxed agent-scope atomics and re-loads only entries whose tag is not
@@ -52,7 +52,6 @@ constexpr unsigned kLdsSpinCap = 1u << 26;  // bounded waits inside the workgrou
 constexpr int kPartStride = HD + 2;      // o[64], m, l
 constexpr int kPairs = QKV / 2;          // RoPE pairs (i, i+32) of every q/k/v head
 constexpr int kLmR = 2;                  // lm_head rows per unit
-constexpr int kNB = 8;                   // lines in flight per loader wave
 static_assert(VOCAB % kLmR == 0, "lm_head units");
 
 enum : unsigned { T_QKV = 0, T_ATT_PART = 1, T_ATT = 2, T_XA = 3, T_ACT = 4, T_X = 5 };
@@ -66,6 +65,9 @@ struct RingCfg {
     static constexpr int SS = kQuant ? S : 1;                  // side-value slots
     static constexpr int LPR2 = Fmt<WT>::CPL;                  // lines per 2048-wide row
     static constexpr int LPR8 = INTER / Fmt<WT>::CPC / kWave;  // lines per 8192-wide row
+    // Lines in flight per loader wave (measured on MI355X: deeper helps bf16, whose rows are 4x
+    // longer; the quantised types, limited by compute, lose a little with it).
+    static constexpr int NB = kQuant ? 8 : 16;
 };
 
 template <WType WT>
@@ -304,10 +306,10 @@ __device__ __forceinline__ float side_value(uint32_t raw) {
     return __builtin_bit_cast(float, raw);
 }
 
-// Loader wave for compute wave `wave`: kNB lines in flight.  Every slot always holds a load (a
+// Loader wave for compute wave `wave`: RingCfg::NB lines in flight.  Every slot always holds a load (a
 // repeat of the last line where the stream has none, at a segment switch or past the end), so the
 // in-order completion count the compiler waits on is exact; each landed line is copied into the
-// ring and published through full[wave].  The segment switch runs once per round of kNB slots.
+// ring and published through full[wave].  The segment switch runs once per round of NB slots.
 template <WType WT>
 __device__ void loader(const DecodeParams& p, Smem<WT>& sm, int wave, int lane) {
     using C = RingCfg<WT>;
@@ -317,9 +319,9 @@ __device__ void loader(const DecodeParams& p, Smem<WT>& sm, int wave, int lane) 
     st.init(&p, gw, NW);
     const int loff = lane * 16;
     const int soff = WT == WType::INT4 ? (lane / 4) * 2 : 0;
-    u32x4 buf[kNB];
-    uint32_t sd[kNB];
-    bool v[kNB];
+    u32x4 buf[C::NB];
+    uint32_t sd[C::NB];
+    bool v[C::NB];
     const char* last = st.cur;
     const char* slast = st.scur;
     auto issue = [&](int s) {
@@ -334,13 +336,13 @@ __device__ void loader(const DecodeParams& p, Smem<WT>& sm, int wave, int lane) 
         if (st.have) st.advance();
     };
 #pragma unroll
-    for (int s = 0; s < kNB; ++s) issue(s);
+    for (int s = 0; s < C::NB; ++s) issue(s);
     int k = 0, cdone = 0;
     bool lbad = false;
     for (;;) {
         bool any = false;
 #pragma unroll
-        for (int s = 0; s < kNB; ++s) {
+        for (int s = 0; s < C::NB; ++s) {
             if (v[s]) {
                 any = true;
                 if (k - cdone >= C::S) {
@@ -960,15 +962,34 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
             lane_inputs<WT, true>(sm.xa, &nw, inv, xr, xsum, lane);
             stamp_in(p, l, 4, 1);
             drain();
-#pragma unroll 1
-            for (int u = gw; u < INTER; u += NW) {
-                Row<WT> rg, ru;
+            // int4 rows are software-pipelined: the next unit's lines are read from the ring
+            // before this unit is computed, hiding the LDS latency.  (Releasing them with the current
+            // ones is safe: the wave's LDS reads execute before its later release store.)  Wider
+            // rows (bf16 4 lines, int8 2) would push the kernel past its registers.
+            constexpr bool kPipe = WT == WType::INT4;
+            Row<WT> rg, ru;
+            if (kPipe && gw < INTER) {
                 take_row<WT>(sm, cs, wave, lane, lbad, rg);
                 take_row<WT>(sm, cs, wave, lane, lbad, ru);
+            }
+#pragma unroll 1
+            for (int u = gw; u < INTER; u += NW) {
+                Row<WT> ng, nu;
+                if (!kPipe) {
+                    take_row<WT>(sm, cs, wave, lane, lbad, rg);
+                    take_row<WT>(sm, cs, wave, lane, lbad, ru);
+                } else if (u + NW < INTER) {
+                    take_row<WT>(sm, cs, wave, lane, lbad, ng);
+                    take_row<WT>(sm, cs, wave, lane, lbad, nu);
+                }
                 const float gv = row_dot<WT>(rg, xr, xsum);
                 const float uv = row_dot<WT>(ru, xr, xsum);
                 release(sm, cs, wave, lane);
                 if (lane == 0) tstore(tact + u, silu(gv) * uv, tg + T_ACT);
+                if constexpr (kPipe) {
+                    rg = ng;
+                    ru = nu;
+                }
             }
         }
         stamp(p, 1 + 6 * l + 4);
@@ -1012,11 +1033,21 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
         float lg = 0.f;
         int lr = 0, nrow = 0;
         drain();
-#pragma unroll 1
-        for (int u = gw; u < VOCAB / kLmR; u += NW) {
-            Row<WT> rr[kLmR];
+        constexpr bool kPipe = WT == WType::INT4;  // software-pipelined as in gate_up
+        Row<WT> rr[kLmR];
+        if (kPipe && gw < VOCAB / kLmR)
 #pragma unroll
             for (int i = 0; i < kLmR; ++i) take_row<WT>(sm, cs, wave, lane, lbad, rr[i]);
+#pragma unroll 1
+        for (int u = gw; u < VOCAB / kLmR; u += NW) {
+            Row<WT> nr[kLmR];
+            if (!kPipe) {
+#pragma unroll
+                for (int i = 0; i < kLmR; ++i) take_row<WT>(sm, cs, wave, lane, lbad, rr[i]);
+            } else if (u + NW < VOCAB / kLmR) {
+#pragma unroll
+                for (int i = 0; i < kLmR; ++i) take_row<WT>(sm, cs, wave, lane, lbad, nr[i]);
+            }
             float d[kLmR];
 #pragma unroll
             for (int i = 0; i < kLmR; ++i) d[i] = row_dot<WT>(rr[i], xr, xsum);
@@ -1039,6 +1070,9 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
                 drain();  // nothing left pending for the hot path
                 nrow = 0;
             }
+            if constexpr (kPipe)
+#pragma unroll
+                for (int i = 0; i < kLmR; ++i) rr[i] = nr[i];
         }
         if (lane < nrow) *glob(p.logits + lr) = lg;
         if (lane == 0) {
