@@ -57,6 +57,13 @@ static_assert(VOCAB % kLmR == 0, "lm_head units");
 enum : unsigned { T_QKV = 0, T_ATT_PART = 1, T_ATT = 2, T_XA = 3, T_ACT = 4, T_X = 5 };
 constexpr unsigned T_ARG = NL * kTagStride;
 
+// Attention tiles in Smem::big (floats): K as fp16 pairs [128][kKs] (16-byte aligned rows whose
+// 128-bit reads by 16 consecutive lanes hit distinct banks), V [128][8] x 16 B, scores [4][128], q [4][64].
+constexpr int kKs = 36;
+constexpr int kAttnV = kAttnChunk * kKs, kAttnP = kAttnV + kAttnChunk * HD / 2, kAttnQ = kAttnP + 4 * kAttnChunk;
+constexpr int kBig = kAttnQ + 4 * HD;
+static_assert(kBig >= INTER, "big holds the down-projection input");
+
 // Ring geometry per weight type.
 template <WType WT>
 struct RingCfg {
@@ -76,7 +83,7 @@ struct Smem {
     float side[kCW][RingCfg<WT>::SS][kWave];
     float xin[H];     // layer input (residual stream)
     float xa[H];      // residual after attention
-    float big[9216];  // attention tiles | attention output | SwiGLU output
+    float big[kBig];  // attention tiles | attention output | SwiGLU output
     float rope_c[HD / 2], rope_s[HD / 2];
     float part[kCW];
     float red_v[kCW];
@@ -384,10 +391,10 @@ template <int N, bool SQ, int SWZ = 0>
 __device__ void fetch(const uint64_t* src, unsigned tag, float* dst, float* part, unsigned* err, int tid) {
     constexpr int PT = N / kCT;
     static_assert(N % kCT == 0, "fetch size");
+    unsigned spins = 0;
     uint64_t v[PT];
 #pragma unroll
     for (int k = 0; k < PT; ++k) v[k] = tload(src + tid + k * kCT);
-    unsigned spins = 0;
     for (;;) {
         bool ok = true;
 #pragma unroll
@@ -599,6 +606,11 @@ constexpr int kInPhase = 100;
 __device__ __forceinline__ void stamp_in(const DecodeParams& p, int l, int phase, int k) {
     if (l == 1) stamp(p, kInPhase + 2 * phase + k);
 }
+// Steps inside the first attention task of layer 1 (slots kAttnSteps + 0..5).
+constexpr int kAttnSteps = 112;
+__device__ __forceinline__ void stamp_attn(const DecodeParams& p, int l, bool first, int k) {
+    if (l == 1 && first) stamp(p, kAttnSteps + k);
+}
 
 // Drain this wave's outstanding global accesses before a row loop.  They are long complete by then
 // (earlier phases' stores); without it the compiler, which cannot tell the loop's first iteration
@@ -668,7 +680,8 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
     const int pos = *glob(p.d_pos);
     const int tok = min(max(*glob(p.d_token), 0), VOCAB - 1);
     const unsigned step = *glob(p.d_step);
-    const unsigned base = step * kEpochStride;
+    // Epochs start at 1: the arena starts zeroed, and a zero tag must never look current.
+    const unsigned base = (step + 1u) * kEpochStride;
     const int ctx = pos + 1;
     const int nsplit = (ctx + kAttnChunk - 1) / kAttnChunk;
     const int NS = p.max_seq / kAttnChunk;
@@ -767,71 +780,83 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
         // ---- split-K attention: task = (kv head, 128-token split), one workgroup per task ----
         renew();
         {
-            uint32_t* Ks = reinterpret_cast<uint32_t*>(sm.big);  // [128][33]
-            u32x4* Vs = reinterpret_cast<u32x4*>(sm.big + 4224);  // [128][8]
-            float* ps = sm.big + 8320;                            // [4][128]
-            float* qs = sm.big + 8832;                            // [4][64]
-            float* kvc = sm.big + 9088;                           // [2][64] this token's k, v
-            constexpr int kTile = kAttnChunk * 8 / kCT;           // 16-byte chunks per thread
+            uint32_t* Ks = reinterpret_cast<uint32_t*>(sm.big);       // [128][kKs] fp16 pairs
+            u32x4* Vs = reinterpret_cast<u32x4*>(sm.big + kAttnV);     // [128][8]
+            float* ps = sm.big + kAttnP;                               // [4][128]
+            float* qs = sm.big + kAttnQ;                               // [4][64]
+            uint16_t* Ks16 = reinterpret_cast<uint16_t*>(Ks);
+            uint16_t* Vs16 = reinterpret_cast<uint16_t*>(Vs);
+            constexpr int kTile = kAttnChunk * 8 / kCT;               // 16-byte chunks per thread
             const int T = NKV * nsplit;
 #pragma unroll 1
             for (int t = blockIdx.x; t < T; t += G) {
                 const int kvh = t % NKV, split = t / NKV;
                 const int t0 = split * kAttnChunk, n = min(kAttnChunk, ctx - t0);
+                const bool first = t == static_cast<int>(blockIdx.x);
+                stamp_attn(p, l, first, 0);
                 const uint16_t* Kg = p.k_cache + l * layer_cache + static_cast<size_t>(kvh) * p.max_seq * HD;
                 const uint16_t* Vg = p.v_cache + l * layer_cache + static_cast<size_t>(kvh) * p.max_seq * HD;
-                // Earlier tokens come from the cache and do not depend on this step: request them first.
-                u32x4 kt[kTile], vt[kTile];
+                // Earlier tokens come from the cache and do not depend on this step: they go into the LDS
+                // tiles while the qkv phase is still finishing elsewhere.
+                {
+                    u32x4 kt[kTile], vt[kTile];
 #pragma unroll
-                for (int k = 0; k < kTile; ++k) {
-                    const int idx = tid + k * kCT, r = idx / 8, c = idx % 8;
-                    if (r < n && t0 + r < pos) {
-                        kt[k] = load_stream(Kg + static_cast<size_t>(t0 + r) * HD + c * 8);
-                        vt[k] = load_stream(Vg + static_cast<size_t>(t0 + r) * HD + c * 8);
-                    }
-                }
-                // q of the group's 4 heads and (last split only) this token's k and v: one wait per thread.
-                qs[tid] = wait1(tqkv + (kvh * 4) * HD + tid, tg + T_QKV, err);
-                if (tid < 2 * HD && t0 + n - 1 == pos)
-                    kvc[tid] = wait1(tqkv + (tid < HD ? NH * HD : (NH + NKV) * HD - HD) + kvh * HD + tid, tg + T_QKV, err);
-                cbar(sm.bar, ep, wave, lane, lbad);
-                if (t == static_cast<int>(blockIdx.x)) stamp_in(p, l, 1, 0);
-#pragma unroll
-                for (int k = 0; k < kTile; ++k) {
-                    const int idx = tid + k * kCT, r = idx / 8, c = idx % 8;
-                    if (r < n) {
-                        u32x4 kv = kt[k], vv = vt[k];
-                        if (t0 + r == pos) {  // rounded to fp16 exactly as the qkv phase wrote the cache
-#pragma unroll
-                            for (int e = 0; e < 4; ++e) {
-                                kv[e] = static_cast<uint32_t>(float_to_half_bits(kvc[c * 8 + 2 * e])) |
-                                        (static_cast<uint32_t>(float_to_half_bits(kvc[c * 8 + 2 * e + 1])) << 16);
-                                vv[e] = static_cast<uint32_t>(float_to_half_bits(kvc[HD + c * 8 + 2 * e])) |
-                                        (static_cast<uint32_t>(float_to_half_bits(kvc[HD + c * 8 + 2 * e + 1])) << 16);
-                            }
+                    for (int k = 0; k < kTile; ++k) {
+                        const int idx = tid + k * kCT, r = idx / 8, c = idx % 8;
+                        if (r < n && t0 + r < pos) {
+                            kt[k] = load_stream(Kg + static_cast<size_t>(t0 + r) * HD + c * 8);
+                            vt[k] = load_stream(Vg + static_cast<size_t>(t0 + r) * HD + c * 8);
                         }
+                    }
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) Ks[r * 33 + c * 4 + e] = kv[e];
-                        Vs[r * 8 + c] = vv;
+                    for (int k = 0; k < kTile; ++k) {
+                        const int idx = tid + k * kCT, r = idx / 8, c = idx % 8;
+                        if (r < n && t0 + r < pos) {
+                            *reinterpret_cast<u32x4*>(Ks + r * kKs + c * 4) = kt[k];
+                            Vs[r * 8 + c] = vt[k];
+                        }
                     }
                 }
+                // q of the group's 4 heads (thread = head-in-group x dim) and, in the split holding this
+                // token, its k and v, rounded to fp16 exactly as the qkv phase wrote them to the cache.
+                qs[tid] = wait1(tqkv + (kvh * 4) * HD + tid, tg + T_QKV, err);
+                if (tid < 2 * HD && t0 + n - 1 == pos) {
+                    const float kv = wait1(tqkv + (tid < HD ? NH * HD : (NH + NKV) * HD - HD) + kvh * HD + tid, tg + T_QKV, err);
+                    const int r = pos - t0;
+                    if (tid < HD) {
+                        Ks16[r * 2 * kKs + tid] = float_to_half_bits(kv);
+                    } else {
+                        Vs16[r * HD + tid - HD] = float_to_half_bits(kv);
+                    }
+                }
+                stamp_attn(p, l, first, 1);
                 cbar(sm.bar, ep, wave, lane, lbad);
+                if (first) stamp_in(p, l, 1, 0);
+                stamp_attn(p, l, first, 2);
                 // wave w = query head kvh*4 + w; lane scores tokens lane and lane + 64.
                 float s[2];
+                {
+                    f32x4 qv[HD / 4];
 #pragma unroll
-                for (int k = 0; k < 2; ++k) {
-                    const int j = lane + kWave * k;
-                    if (j < n) {
-                        float dot = 0.f;
+                    for (int i = 0; i < HD / 4; ++i) qv[i] = *reinterpret_cast<const f32x4*>(qs + wave * HD + 4 * i);
 #pragma unroll
-                        for (int d2 = 0; d2 < HD / 2; ++d2) {
-                            const uint32_t kk = Ks[j * 33 + d2];
-                            dot = fmaf(half_bits_to_float(static_cast<uint16_t>(kk)), qs[wave * HD + 2 * d2], dot);
-                            dot = fmaf(half_bits_to_float(static_cast<uint16_t>(kk >> 16)), qs[wave * HD + 2 * d2 + 1], dot);
+                    for (int k = 0; k < 2; ++k) {
+                        const int j = lane + kWave * k;
+                        if (j < n) {
+                            float dot = 0.f;
+#pragma unroll
+                            for (int i = 0; i < HD / 8; ++i) {
+                                const u32x4 kk = *reinterpret_cast<const u32x4*>(Ks + j * kKs + 4 * i);
+#pragma unroll
+                                for (int e = 0; e < 4; ++e) {
+                                    dot = fmaf(half_bits_to_float(static_cast<uint16_t>(kk[e])), qv[2 * i + e / 2][2 * (e % 2)], dot);
+                                    dot = fmaf(half_bits_to_float(static_cast<uint16_t>(kk[e] >> 16)), qv[2 * i + e / 2][2 * (e % 2) + 1], dot);
+                                }
+                            }
+                            s[k] = 0.125f * dot;
+                        } else {
+                            s[k] = -INFINITY;
                         }
-                        s[k] = 0.125f * dot;
-                    } else {
-                        s[k] = -INFINITY;
                     }
                 }
                 const float m = wave_max(fmaxf(s[0], s[1]));
@@ -840,23 +865,23 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
                 const float lsum = wave_sum(p0 + p1);
                 ps[wave * kAttnChunk + lane] = p0;
                 ps[wave * kAttnChunk + lane + kWave] = p1;
+                stamp_attn(p, l, first, 3);
                 // P.V: lane = (token phase g, 8-column group c) takes tokens g, g+8, ... of columns
                 // 8c..8c+7; the 8 token phases are then summed across lanes.
                 const int g = lane >> 3, c = lane & 7;
                 float o[8];
 #pragma unroll
                 for (int e = 0; e < 8; ++e) o[e] = 0.f;
+                const int iters = (n - g + 7) / 8;  // tokens g + 8 i < n
 #pragma unroll 4
-                for (int i = 0; i < kAttnChunk / 8; ++i) {
+                for (int i = 0; i < iters; ++i) {
                     const int j = g + 8 * i;
-                    if (j < n) {
-                        const float pj = ps[wave * kAttnChunk + j];
-                        const u32x4 vv = Vs[j * 8 + c];
+                    const float pj = ps[wave * kAttnChunk + j];
+                    const u32x4 vv = Vs[j * 8 + c];
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            o[2 * e] = fmaf(pj, half_bits_to_float(static_cast<uint16_t>(vv[e])), o[2 * e]);
-                            o[2 * e + 1] = fmaf(pj, half_bits_to_float(static_cast<uint16_t>(vv[e] >> 16)), o[2 * e + 1]);
-                        }
+                    for (int e = 0; e < 4; ++e) {
+                        o[2 * e] = fmaf(pj, half_bits_to_float(static_cast<uint16_t>(vv[e])), o[2 * e]);
+                        o[2 * e + 1] = fmaf(pj, half_bits_to_float(static_cast<uint16_t>(vv[e] >> 16)), o[2 * e + 1]);
                     }
                 }
 #pragma unroll
@@ -881,7 +906,9 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
                         }
                     }
                 }
-                cbar(sm.bar, ep, wave, lane, lbad);  // the tiles are overwritten next
+                stamp_attn(p, l, first, 4);
+                cbar(sm.bar, ep, wave, lane, lbad);  // the tiles are overwritten next (or by the wo input)
+                stamp_attn(p, l, first, 5);
             }
         }
         stamp(p, 1 + 6 * l + 1);
