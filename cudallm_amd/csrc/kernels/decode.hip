@@ -61,7 +61,10 @@ constexpr unsigned T_ARG = NL * kTagStride;
 // 128-bit reads by 16 consecutive lanes hit distinct banks), V [128][8] x 16 B, scores [4][128], q [4][64].
 constexpr int kKs = 36;
 constexpr int kAttnV = kAttnChunk * kKs, kAttnP = kAttnV + kAttnChunk * HD / 2, kAttnQ = kAttnP + 4 * kAttnChunk;
-constexpr int kBig = kAttnQ + 4 * HD;
+// The digit table of the integer dot products sits after the down-projection input: a wave can be
+// fetching that input (next phase) while another still reads the table.
+constexpr int kDigOff = INTER, kDigWordsMax = 3 * 512;
+constexpr int kBig = kAttnQ + 4 * HD > kDigOff + kDigWordsMax ? kAttnQ + 4 * HD : kDigOff + kDigWordsMax;
 static_assert(kBig >= INTER, "big holds the down-projection input");
 
 // Ring geometry per weight type.
@@ -72,9 +75,9 @@ struct RingCfg {
     static constexpr int SS = kQuant ? S : 1;                  // side-value slots
     static constexpr int LPR2 = Fmt<WT>::CPL;                  // lines per 2048-wide row
     static constexpr int LPR8 = INTER / Fmt<WT>::CPC / kWave;  // lines per 8192-wide row
-    // Lines in flight per loader wave (measured on MI355X: deeper helps bf16, whose rows are 4x
-    // longer; the quantised types, limited by compute, lose a little with it).
-    static constexpr int NB = kQuant ? 8 : 16;
+    // Lines in flight per loader wave (measured on MI355X: bf16 16, int8 12, int4 8; deeper queues
+    // also delay the small polling loads of the phase handoffs behind them).
+    static constexpr int NB = WT == WType::BF16 ? 16 : WT == WType::INT8 ? 12 : 8;
 };
 
 template <WType WT>
@@ -86,6 +89,7 @@ struct Smem {
     float big[kBig];  // attention tiles | attention output | SwiGLU output
     float rope_c[HD / 2], rope_s[HD / 2];
     float part[kCW];
+    float pmax[kCW];  // per-wave max |x g| of the last fetch with MXG
     float red_v[kCW];
     int red_i[kCW];
     unsigned bar[kCW];
@@ -387,11 +391,20 @@ __device__ __forceinline__ int swz(int i) {
 // The whole compute group copies N tagged floats into LDS once every tag equals `tag` (at swz<SWZ>
 // positions when SWZ > 0); with SQ, each wave also leaves the sum of squares of the values it
 // copied in part[wave].  Callers follow with cbar().
-template <int N, bool SQ, int SWZ = 0>
-__device__ void fetch(const uint64_t* src, unsigned tag, float* dst, float* part, unsigned* err, int tid) {
+//
+// With MXG, each wave also leaves max |x_i g_i| over the entries it copied in pmax[wave] (g: the
+// norm weights, read while the wait runs), from which the fixed-point scale of the integer dot
+// products is derived.
+template <int N, bool SQ, int SWZ = 0, bool MXG = false>
+__device__ void fetch(const uint64_t* src, unsigned tag, float* dst, float* part, unsigned* err, int tid,
+                      const float* g = nullptr, float* pmax = nullptr) {
     constexpr int PT = N / kCT;
     static_assert(N % kCT == 0, "fetch size");
     unsigned spins = 0;
+    float gv[MXG ? PT : 1];
+    if constexpr (MXG)
+#pragma unroll
+        for (int k = 0; k < PT; ++k) gv[k] = gload(g + tid + k * kCT);
     uint64_t v[PT];
 #pragma unroll
     for (int k = 0; k < PT; ++k) v[k] = tload(src + tid + k * kCT);
@@ -404,7 +417,7 @@ __device__ void fetch(const uint64_t* src, unsigned tag, float* dst, float* part
         for (int k = 0; k < PT; ++k)
             if (!tagged(v[k], tag)) v[k] = tload(src + tid + k * kCT);
     }
-    float ss = 0.f;
+    float ss = 0.f, mx = 0.f;
 #pragma unroll
     for (int k = 0; k < PT; ++k) {
         const float x = tvalue(v[k]);
@@ -415,10 +428,15 @@ __device__ void fetch(const uint64_t* src, unsigned tag, float* dst, float* part
             dst[i] = x;
         }
         ss += x * x;
+        if constexpr (MXG) mx = fmaxf(mx, fabsf(x * gv[k]));
     }
     if constexpr (SQ) {
         ss = wave_sum(ss);
         if ((tid & (kWave - 1)) == 0) part[tid / kWave] = ss;
+    }
+    if constexpr (MXG) {
+        mx = wave_max(mx);
+        if ((tid & (kWave - 1)) == 0) pmax[tid / kWave] = mx;
     }
 }
 
@@ -430,8 +448,106 @@ __device__ __forceinline__ float rms_inv(const float* part, float eps) {
     return rsqrtf(ss / static_cast<float>(H) + eps);
 }
 
-// Norm weights of the lane's 32 columns of a 2048-wide row (same column mapping as the matvec).
 typedef const __attribute__((address_space(1))) f32x4 global_f32x4;
+
+// ---- integer dot products for the quantised weights (gate_up and lm_head) ----------------------
+//
+// The normalised input x^ = (x inv) g is written as a 22-bit fixed-point integer with one power-of-two
+// scale per phase, xi = rint(x^ 2^e) (|xi| <= 2^22), and split into signed digits: three base-256
+// digits (bytes) for int8 weights, six base-16 digits (nibbles) for int4 weights, packed in the
+// weights' own layout so that v_dot4_i32_i8 / v_dot8_i32_i4 multiply raw weight words.  The integer
+// partial sums are exact; the only new rounding is that of xi (at most 2^-23 of max |x^|), against
+// fp32's 2^-24 of each |x^|.  Adding the offset C = (base/2) * (1 + base + base^2 ...) makes every digit
+// of xi + C non-negative, and xor C then turns each of them into its signed two's-complement form.
+template <WType WT>
+struct Dig {
+    static constexpr int ND = WT == WType::INT8 ? 3 : 6;      // digits
+    static constexpr int WPD = 2048 / (WT == WType::INT8 ? 4 : 8);  // digit words per digit (2048 columns)
+    static constexpr uint32_t C = WT == WType::INT8 ? 0x808080u : 0x888888u;
+    uint32_t d[24];  // the lane's words: int8 [digit][chunk][word], int4 [digit][word]
+};
+static_assert(Dig<WType::INT8>::ND * Dig<WType::INT8>::WPD == Dig<WType::INT4>::ND * Dig<WType::INT4>::WPD,
+              "digit tables share one size");
+static_assert(Dig<WType::INT8>::ND * Dig<WType::INT8>::WPD == kDigWordsMax, "digit table size");
+
+// Exponent e of the fixed-point scale from a bound m >= max |x^|: m 2^e < 2^22.
+__device__ __forceinline__ int dig_exponent(float m) {
+    if (!(m > 0.f) || !(m < INFINITY)) return 0;
+    return 21 - ilogbf(m);
+}
+
+// Thread tid writes the digit words of columns 8 tid .. 8 tid + 7 (all 2048 by the compute group).
+template <WType WT>
+__device__ void make_digits(const float* x, const float* g, float inv, int e, uint32_t* tab, int tid) {
+    using D = Dig<WT>;
+    const f32x4 x0 = reinterpret_cast<const f32x4*>(x)[2 * tid], x1 = reinterpret_cast<const f32x4*>(x)[2 * tid + 1];
+    const f32x4 g0 = *((global_f32x4*)g + 2 * tid), g1 = *((global_f32x4*)g + 2 * tid + 1);
+    uint32_t u[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+        const float xc = c < 4 ? x0[c] : x1[c - 4];
+        const float gc = c < 4 ? g0[c] : g1[c - 4];
+        const int xi = static_cast<int>(rintf(ldexpf(xc * inv * gc, e)));
+        u[c] = (static_cast<uint32_t>(xi) + D::C) ^ D::C;
+    }
+    if constexpr (WT == WType::INT8) {
+#pragma unroll
+        for (int k = 0; k < 3; ++k)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                uint32_t w = 0;
+#pragma unroll
+                for (int b = 0; b < 4; ++b) w |= ((u[4 * h + b] >> (8 * k)) & 0xffu) << (8 * b);
+                tab[k * D::WPD + 2 * tid + h] = w;
+            }
+    } else {
+#pragma unroll
+        for (int k = 0; k < 6; ++k) {
+            uint32_t w = 0;
+#pragma unroll
+            for (int b = 0; b < 8; ++b) w |= ((u[b] >> (4 * k)) & 0xfu) << (4 * b);
+            tab[k * D::WPD + tid] = w;
+        }
+    }
+}
+
+// The lane's digit words (same column mapping as its weight chunks).
+template <WType WT>
+__device__ __forceinline__ void load_digits(const uint32_t* tab, int lane, Dig<WT>& dg) {
+    using D = Dig<WT>;
+    if constexpr (WT == WType::INT8) {
+#pragma unroll
+        for (int k = 0; k < 3; ++k)
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+                const u32x4 v = *reinterpret_cast<const u32x4*>(tab + k * D::WPD + (c * kWave + lane) * 4);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) dg.d[(k * 2 + c) * 4 + i] = v[i];
+            }
+    } else {
+#pragma unroll
+        for (int k = 0; k < 6; ++k) {
+            const u32x4 v = *reinterpret_cast<const u32x4*>(tab + k * D::WPD + lane * 4);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) dg.d[k * 4 + i] = v[i];
+        }
+    }
+}
+
+// After the fetch of a normalised phase input (and its barrier): the scale exponent from the waves'
+// max |x g| and inv, and this thread's digit words into the table.  Returns 2^-e.  Callers follow
+// with a barrier, then load_digits().
+template <WType WT, typename SM>
+__device__ __forceinline__ float digits_prologue(SM& sm, float inv, const float* g, int tid, const float* x = nullptr) {
+    float m = 0.f;
+#pragma unroll
+    for (int w = 0; w < kCW; ++w) m = fmaxf(m, sm.pmax[w]);
+    const int e = dig_exponent(m * inv);
+    make_digits<WT>(x ? x : sm.xa, g, inv, e, reinterpret_cast<uint32_t*>(sm.big + kDigOff), tid);
+    return ldexpf(1.f, -e);
+}
+
+// Norm weights of the lane's 32 columns of a 2048-wide row (same column mapping as the matvec).
 template <WType WT>
 struct NormW {
     f32x4 v[Fmt<WT>::CPL * Fmt<WT>::CPC / 4];
@@ -507,6 +623,40 @@ __device__ __forceinline__ float row_dot(const Row<WT>& r, const float* xr, floa
     s = wave_sum(s);
     if constexpr (WT == WType::INT8) s *= r.s;
     return s;
+}
+
+// Complete dot of a 2048-wide quantised row against the input digits, uniform across the wave;
+// `sc` = 2^-e.  int8: sum_k 256^k sum(q d_k), times the row scale; int4: sum_k 16^k sum(q d_k) per lane
+// (the stored nibble u = q + 8 becomes q by xor 8), times the lane's group scale.
+template <WType WT>
+__device__ __forceinline__ float row_dot_dig(const Row<WT>& r, const Dig<WT>& dg, float sc) {
+    if constexpr (WT == WType::INT8) {
+        int a0 = 0, a1 = 0, a2 = 0;
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int w = static_cast<int>(r.w[c][i]);
+                a0 = __builtin_amdgcn_sdot4(w, static_cast<int>(dg.d[(0 * 2 + c) * 4 + i]), a0, false);
+                a1 = __builtin_amdgcn_sdot4(w, static_cast<int>(dg.d[(1 * 2 + c) * 4 + i]), a1, false);
+                a2 = __builtin_amdgcn_sdot4(w, static_cast<int>(dg.d[(2 * 2 + c) * 4 + i]), a2, false);
+            }
+        float t = fmaf(fmaf(static_cast<float>(a2), 256.f, static_cast<float>(a1)), 256.f, static_cast<float>(a0));
+        t = wave_sum(t);
+        return t * sc * r.s;
+    } else {
+        int a[6] = {0, 0, 0, 0, 0, 0};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int w = static_cast<int>(r.w[0][i] ^ 0x88888888u);
+#pragma unroll
+            for (int k = 0; k < 6; ++k) a[k] = __builtin_amdgcn_sdot8(w, static_cast<int>(dg.d[k * 4 + i]), a[k], false);
+        }
+        const int p0 = a[0] + 16 * a[1], p1 = a[2] + 16 * a[3], p2 = a[4] + 16 * a[5];
+        float t = fmaf(static_cast<float>(p2), 65536.f, static_cast<float>(p0 + 256 * p1));
+        t = wave_sum(t * r.s);
+        return t * sc;
+    }
 }
 
 // Per-chunk sums of the lane's down-projection inputs (the bias correction of quantised chunks);
@@ -659,6 +809,7 @@ template <WType WT>
 __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
     using F = Fmt<WT>;
     constexpr int NX = F::CPL * F::CPC;
+    constexpr bool kDig = WT != WType::BF16;  // gate_up and lm_head use the integer dot products
     __shared__ Smem<WT> sm;
 
     if (threadIdx.x < kCW) {
@@ -980,13 +1131,25 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
         renew();
         {
             NormW<WT> nw;
-            load_norm<WT>(Lw.ffn_norm, lane, nw);
-            fetch<H, true>(txa, tg + T_XA, sm.xa, sm.part, err, tid);
-            cbar(sm.bar, ep, wave, lane, lbad);
-            stamp_in(p, l, 4, 0);
-            const float inv = rms_inv(sm.part, p.eps);
-            float xr[NX], xsum;
-            lane_inputs<WT, true>(sm.xa, &nw, inv, xr, xsum, lane);
+            float xr[kDig ? 1 : NX], xsum = 0.f;
+            Dig<WT> dg;
+            float dsc = 0.f;
+            if constexpr (kDig) {
+                fetch<H, true, 0, true>(txa, tg + T_XA, sm.xa, sm.part, err, tid, Lw.ffn_norm, sm.pmax);
+                cbar(sm.bar, ep, wave, lane, lbad);
+                stamp_in(p, l, 4, 0);
+                const float inv = rms_inv(sm.part, p.eps);
+                dsc = digits_prologue<WT>(sm, inv, Lw.ffn_norm, tid);
+                cbar(sm.bar, ep, wave, lane, lbad);
+                load_digits<WT>(reinterpret_cast<const uint32_t*>(sm.big + kDigOff), lane, dg);
+            } else {
+                load_norm<WT>(Lw.ffn_norm, lane, nw);
+                fetch<H, true>(txa, tg + T_XA, sm.xa, sm.part, err, tid);
+                cbar(sm.bar, ep, wave, lane, lbad);
+                stamp_in(p, l, 4, 0);
+                const float inv = rms_inv(sm.part, p.eps);
+                lane_inputs<WT, true>(sm.xa, &nw, inv, xr, xsum, lane);
+            }
             stamp_in(p, l, 4, 1);
             drain();
             // int4 rows are software-pipelined: the next unit's lines are read from the ring
@@ -1009,8 +1172,14 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
                     take_row<WT>(sm, cs, wave, lane, lbad, ng);
                     take_row<WT>(sm, cs, wave, lane, lbad, nu);
                 }
-                const float gv = row_dot<WT>(rg, xr, xsum);
-                const float uv = row_dot<WT>(ru, xr, xsum);
+                float gv, uv;
+                if constexpr (kDig) {
+                    gv = row_dot_dig<WT>(rg, dg, dsc);
+                    uv = row_dot_dig<WT>(ru, dg, dsc);
+                } else {
+                    gv = row_dot<WT>(rg, xr, xsum);
+                    uv = row_dot<WT>(ru, xr, xsum);
+                }
                 release(sm, cs, wave, lane);
                 if (lane == 0) tstore(tact + u, silu(gv) * uv, tg + T_ACT);
                 if constexpr (kPipe) {
@@ -1047,12 +1216,25 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
     renew();
     {
         NormW<WT> nw;
-        load_norm<WT>(p.final_norm, lane, nw);
-        fetch<H, true>(p.tx + static_cast<size_t>(NL) * H, base + (NL - 1) * kTagStride + T_X, sm.xin, sm.part, err, tid);
-        cbar(sm.bar, ep, wave, lane, lbad);
-        const float inv = rms_inv(sm.part, p.eps);
-        float xr[NX], xsum;
-        lane_inputs<WT, true>(sm.xin, &nw, inv, xr, xsum, lane);
+        float xr[kDig ? 1 : NX], xsum = 0.f;
+        Dig<WT> dg;
+        float dsc = 0.f;
+        const uint64_t* tfin = p.tx + static_cast<size_t>(NL) * H;
+        const unsigned tagfin = base + (NL - 1) * kTagStride + T_X;
+        if constexpr (kDig) {
+            fetch<H, true, 0, true>(tfin, tagfin, sm.xin, sm.part, err, tid, p.final_norm, sm.pmax);
+            cbar(sm.bar, ep, wave, lane, lbad);
+            const float inv = rms_inv(sm.part, p.eps);
+            dsc = digits_prologue<WT>(sm, inv, p.final_norm, tid, sm.xin);
+            cbar(sm.bar, ep, wave, lane, lbad);
+            load_digits<WT>(reinterpret_cast<const uint32_t*>(sm.big + kDigOff), lane, dg);
+        } else {
+            load_norm<WT>(p.final_norm, lane, nw);
+            fetch<H, true>(tfin, tagfin, sm.xin, sm.part, err, tid);
+            cbar(sm.bar, ep, wave, lane, lbad);
+            const float inv = rms_inv(sm.part, p.eps);
+            lane_inputs<WT, true>(sm.xin, &nw, inv, xr, xsum, lane);
+        }
         float bv = -INFINITY;
         int bi = 0x7fffffff;
         // Logits are collected across lanes (lane j holds the wave's j-th row) and stored 64 at a time:
@@ -1077,7 +1259,13 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
             }
             float d[kLmR];
 #pragma unroll
-            for (int i = 0; i < kLmR; ++i) d[i] = row_dot<WT>(rr[i], xr, xsum);
+            for (int i = 0; i < kLmR; ++i) {
+                if constexpr (kDig) {
+                    d[i] = row_dot_dig<WT>(rr[i], dg, dsc);
+                } else {
+                    d[i] = row_dot<WT>(rr[i], xr, xsum);
+                }
+            }
             release(sm, cs, wave, lane);
 #pragma unroll
             for (int i = 0; i < kLmR; ++i) {
