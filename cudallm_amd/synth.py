@@ -59,14 +59,19 @@ def _specs(wdtype: str, d: dict) -> list[tuple[str, int, int, int]]:
     return s
 
 
-def write_model(path, wdtype: str, seed: int = 0, device: str | None = None) -> int:
+def write_model(path, wdtype: str, seed: int = 0, device: str | None = None, max_seq_len: int | None = None) -> int:
     """Write a seeded Llama-3.2-1B-shaped model; returns the file's weight bytes (sum of nbytes).
 
     The bf16 master depends only on ``seed`` (and the device's generator), not on ``wdtype``.
+    ``max_seq_len`` (default 4096) is the header's context limit; the weights do not depend on it.
     """
     if wdtype not in ("bf16", "int8", "int4"):
         raise ValueError("wdtype must be bf16, int8 or int4")
     d = dict(LLAMA_1B)
+    if max_seq_len is not None:
+        if max_seq_len <= 0 or max_seq_len % 128:
+            raise ValueError("max_seq_len must be a positive multiple of 128")
+        d["max_seq_len"] = int(max_seq_len)
     dev = torch.device(device or ("cuda" if torch.cuda.is_available() else "cpu"))
     gen = torch.Generator(device=dev)
     gen.manual_seed(seed)

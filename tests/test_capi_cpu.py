@@ -269,3 +269,19 @@ def test_other_hook_argument_errors(lib):
     with pytest.raises(E.CudaLLMError) as ei:
         E.kernel_argmax(np.zeros(0, np.float32))
     assert ei.value.code == INVALID_ARG
+
+
+def test_bench_suites_mirror_the_reference():
+    """The decode suites follow the reference's bench/bench_decode.py:12-26 (names, options, lengths) and its
+    prompt (src/tools/cudallm_bench.cpp:24)."""
+    from cudallm_amd import bench_decode as B
+    assert [e[0] for e in B.ABLATION] == ["A0_naive", "A1_matvec_opt", "A2_attn_opt", "A3_fused", "A4_graph_nofuse",
+                                          "A5_full"]
+    assert B.ABLATION[0][1:] == ("bf16", "naive", "naive", 0, 0, 128, 256, 5)
+    assert B.ABLATION[-1][1:] == ("bf16", "opt", "opt", 1, 1, 128, 256, 5)
+    assert [e[0] for e in B.QUANT] == ["Q_bf16", "Q_int8", "Q_int4"]
+    assert [e[6] for e in B.CONTEXT] == [128, 128, 512, 512, 1024, 1024, 2048, 2048, 4000, 4000]
+    assert all(e[7] == 32 and e[8] == 3 for e in B.CONTEXT)
+    assert [e[6:8] for e in B.TG] == [(1, 256)] * 3
+    assert all(e[6] + e[7] <= B.LONG_MAX_SEQ for e in B.LONG)
+    assert [B.prompt_token(i) for i in (0, 1, 2, 15152)] == [128000, 8919, 16838, 1000 + (15152 * 7919) % 120000]
