@@ -51,6 +51,22 @@ struct DecodeParams {
     float* residuals;  // optional [(n_layers + 1) * hidden] snapshots (step_debug)
     unsigned long long* stamps;  // optional [grid][kStampSlots] phase-end timestamps (100 MHz clock)
     float eps;
+    // Timing perturbation for tests, 0 in normal use (the CUDALLM_STALL environment variable): bit k
+    // (kStall*) makes each workgroup's compute waves sleep about 13 us before that phase waits for its
+    // input, kStallLoader makes each loader wave sleep at every segment switch, and kStallOdd limits
+    // the sleeps to odd workgroups.  Results must stay bit-identical under any mask.
+    unsigned stall;
+};
+
+enum : unsigned {
+    kStallQkv = 1u << 0,
+    kStallAttn = 1u << 1,
+    kStallWo = 1u << 2,
+    kStallGateUp = 1u << 3,
+    kStallDown = 1u << 4,
+    kStallLmHead = 1u << 5,
+    kStallLoader = 1u << 6,
+    kStallOdd = 1u << 7,
 };
 
 // Timestamp slots per workgroup: 0 = start, 1 + 6 l + k = end of phase k of layer l

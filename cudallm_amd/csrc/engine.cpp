@@ -135,6 +135,8 @@ Engine::Engine(const std::string& path, const EngineOptions& opts) : opts_(opts)
         dp_.residuals = nullptr;
         dp_.stamps = nullptr;
         dp_.eps = c.rms_eps;
+        const char* stall = std::getenv("CUDALLM_STALL");  // timing perturbation for tests only
+        dp_.stall = stall ? static_cast<unsigned>(std::strtoul(stall, nullptr, 0)) : 0u;
         CLLM_HIP(hipDeviceSynchronize());
     } catch (...) {
         release();

@@ -156,6 +156,15 @@ __device__ __forceinline__ float wait1(const uint64_t* a, unsigned tag, unsigned
     return tvalue(v);
 }
 
+// Test hook: sleep about 13 us when the stall mask selects `bit` (and this workgroup, with kStallOdd).
+// The mask is a kernel argument, so the test is a scalar branch that normal runs never take.
+__device__ __forceinline__ void stall_at(const DecodeParams& p, unsigned bit) {
+    if ((p.stall & bit) && (!(p.stall & kStallOdd) || (blockIdx.x & 1))) {
+#pragma unroll 1
+        for (int i = 0; i < 4; ++i) __builtin_amdgcn_s_sleep(127);
+    }
+}
+
 // ---- workgroup-local synchronisation (LDS) ---------------------------------------------------
 
 // The flags below only order LDS accesses, and the LDS executes a wave's accesses in issue order,
@@ -371,7 +380,10 @@ __device__ void loader(const DecodeParams& p, Smem<WT>& sm, int wave, int lane) 
             }
             issue(s);
         }
-        if (!st.have && !st.end) st.next_seg();
+        if (!st.have && !st.end) {
+            stall_at(p, kStallLoader);
+            st.next_seg();
+        }
         if (!any && st.end) break;
     }
     if (lbad) fail(err);
@@ -890,6 +902,7 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
         {
             NormW<WT> nw;
             load_norm<WT>(Lw.attn_norm, lane, nw);
+            stall_at(p, kStallQkv);
             if (l > 0) {
                 fetch<H, true>(p.tx + static_cast<size_t>(l) * H, tg - kTagStride + T_X, sm.xin, sm.part, err, tid);
                 cbar(sm.bar, ep, wave, lane, lbad);
@@ -939,6 +952,7 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
             uint16_t* Vs16 = reinterpret_cast<uint16_t*>(Vs);
             constexpr int kTile = kAttnChunk * 8 / kCT;               // 16-byte chunks per thread
             const int T = NKV * nsplit;
+            stall_at(p, kStallAttn);
 #pragma unroll 1
             for (int t = blockIdx.x; t < T; t += G) {
                 const int kvh = t % NKV, split = t / NKV;
@@ -1109,6 +1123,7 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
         // ---- wo + residual ----
         renew();
         {
+            stall_at(p, kStallWo);
             fetch<H, false>(tatt, tg + T_ATT, sm.big, sm.part, err, tid);
             cbar(sm.bar, ep, wave, lane, lbad);
             stamp_in(p, l, 3, 0);
@@ -1134,6 +1149,7 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
             float xr[kDig ? 1 : NX], xsum = 0.f;
             Dig<WT> dg;
             float dsc = 0.f;
+            stall_at(p, kStallGateUp);
             if constexpr (kDig) {
                 fetch<H, true, 0, true>(txa, tg + T_XA, sm.xa, sm.part, err, tid, Lw.ffn_norm, sm.pmax);
                 cbar(sm.bar, ep, wave, lane, lbad);
@@ -1152,26 +1168,15 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
             }
             stamp_in(p, l, 4, 1);
             drain();
-            // int4 rows are software-pipelined: the next unit's lines are read from the ring
-            // before this unit is computed, hiding the LDS latency.  (Releasing them with the current
-            // ones is safe: the wave's LDS reads execute before its later release store.)  Wider
-            // rows (bf16 4 lines, int8 2) would push the kernel past its registers.
-            constexpr bool kPipe = WT == WType::INT4;
-            Row<WT> rg, ru;
-            if (kPipe && gw < INTER) {
-                take_row<WT>(sm, cs, wave, lane, lbad, rg);
-                take_row<WT>(sm, cs, wave, lane, lbad, ru);
-            }
+            // Not software-pipelined (unlike lm_head): holding the next unit's rows across the
+            // iteration pushed the int4 kernel into VGPR spills, and that build gave wrong, run-to-run
+            // varying results once the loader ran a layer ahead (a 13 us stall before the down
+            // projection's input was enough).  The pipelined form saved 1.6 us per int4 step.
 #pragma unroll 1
             for (int u = gw; u < INTER; u += NW) {
-                Row<WT> ng, nu;
-                if (!kPipe) {
-                    take_row<WT>(sm, cs, wave, lane, lbad, rg);
-                    take_row<WT>(sm, cs, wave, lane, lbad, ru);
-                } else if (u + NW < INTER) {
-                    take_row<WT>(sm, cs, wave, lane, lbad, ng);
-                    take_row<WT>(sm, cs, wave, lane, lbad, nu);
-                }
+                Row<WT> rg, ru;
+                take_row<WT>(sm, cs, wave, lane, lbad, rg);
+                take_row<WT>(sm, cs, wave, lane, lbad, ru);
                 float gv, uv;
                 if constexpr (kDig) {
                     gv = row_dot_dig<WT>(rg, dg, dsc);
@@ -1182,10 +1187,6 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
                 }
                 release(sm, cs, wave, lane);
                 if (lane == 0) tstore(tact + u, silu(gv) * uv, tg + T_ACT);
-                if constexpr (kPipe) {
-                    rg = ng;
-                    ru = nu;
-                }
             }
         }
         stamp(p, 1 + 6 * l + 4);
@@ -1193,6 +1194,7 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
         // ---- down + residual (8192-wide rows, inputs read from LDS) ----
         renew();
         {
+            stall_at(p, kStallDown);
             fetch<INTER, false, F::CPC>(tact, tg + T_ACT, sm.big, sm.part, err, tid);
             cbar(sm.bar, ep, wave, lane, lbad);
             stamp_in(p, l, 5, 0);
@@ -1221,6 +1223,7 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
         float dsc = 0.f;
         const uint64_t* tfin = p.tx + static_cast<size_t>(NL) * H;
         const unsigned tagfin = base + (NL - 1) * kTagStride + T_X;
+        stall_at(p, kStallLmHead);
         if constexpr (kDig) {
             fetch<H, true, 0, true>(tfin, tagfin, sm.xin, sm.part, err, tid, p.final_norm, sm.pmax);
             cbar(sm.bar, ep, wave, lane, lbad);
@@ -1242,7 +1245,10 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
         float lg = 0.f;
         int lr = 0, nrow = 0;
         drain();
-        constexpr bool kPipe = WT == WType::INT4;  // software-pipelined as in gate_up
+        // int4 rows are software-pipelined: the next unit's lines are read from the ring before this
+        // unit is computed, hiding the LDS latency (they are released with the current ones, after
+        // the wave's reads of them).  Wider rows (bf16 4 lines, int8 2) would not fit the registers.
+        constexpr bool kPipe = WT == WType::INT4;
         Row<WT> rr[kLmR];
         if (kPipe && gw < VOCAB / kLmR)
 #pragma unroll

@@ -244,3 +244,29 @@ def test_persistent_long_context_matches_multikernel(wd, model_path, monkeypatch
     finally:
         eng.close()
         ref.close()
+
+
+# Stall masks (bits of DecodeParams::stall in cudallm_amd/csrc/decode.h): before the down projection's
+# input wait (the loader then runs a layer ahead), the loaders at their segment switches, odd
+# workgroups only (skew between workgroups), and every point at once.
+STALLS = {"down": 0x10, "loader": 0x40, "odd_down": 0x90, "all": 0x7F, "odd_all": 0xFF}
+
+
+@pytest.mark.parametrize("wd", ["bf16", "int8", "int4"])
+def test_stalls_leave_results_bit_identical(wd, model_path, engine_runs, monkeypatch):
+    """Timing perturbation of the persistent kernel, a race check of its cross-workgroup handoffs and
+    weight rings: ~13 us sleeps at the selected points change which workgroup, wave or loader runs
+    ahead.  The kernel's reductions have a fixed order, so any difference from the unstalled run is a
+    race.  Teacher-forced over the first 8 tokens through step_debug (residuals and logits)."""
+    base = engine_runs((wd, "opt", "opt", 1, 0))
+    for name, mask in STALLS.items():
+        monkeypatch.setenv("CUDALLM_STALL", hex(mask))
+        try:
+            with E.Engine(model_path(wd), cuda_graph=False) as eng:
+                logits, res, _ = _run(eng, TOKENS[:8], graph=False)
+        finally:
+            monkeypatch.delenv("CUDALLM_STALL")
+        same = bool(np.array_equal(logits, base["logits"][:8]) and np.array_equal(res, base["res"][:8]))
+        print(f"[engine] {wd} stall {name} ({mask:#x}): bit-identical {same}", flush=True)
+        np.testing.assert_array_equal(res, base["res"][:8], err_msg=f"stall {name}")
+        np.testing.assert_array_equal(logits, base["logits"][:8], err_msg=f"stall {name}")
