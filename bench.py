@@ -20,7 +20,6 @@ algorithm restated, oracle/model.py) timed on this host.
 """
 import argparse
 import json
-import math
 import os
 import sys
 import tempfile
@@ -31,6 +30,8 @@ import numpy as np
 
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
+
+from cudallm_amd.kernelbench import SHAPES, bench_matvec, weighted_us  # noqa: E402
 
 METRIC = "batch-1 decode tok/s (bf16/int8/int4) + matvec HBM GB/s as % of peak"
 PEAK_HBM = 8.0e12  # MI355X HBM3E, bytes/s
@@ -80,71 +81,6 @@ def bench_decode(path, wd: str, steps: int, warmup: int, torch) -> dict:
             "gbps": bpt * tok_s / 1e9, "frac_of_8tbs": bpt * tok_s / PEAK_HBM,
             "roofline_tok_s": PEAK_HBM / bpt, "context": [ctx0, ctx0 + steps], "load_s": round(load_s, 2),
             "last_token": nxt, "kernel_avg_us": ev_us, "kernel_gbps": bpt / ev_us / 1e3}
-
-
-SHAPES = [("qkv", 3072, 2048, "store", True), ("wo", 2048, 2048, "add", False),
-          ("gate_up", 16384, 2048, "swiglu", True), ("down", 2048, 8192, "add", False),
-          ("lm_head", 128256, 2048, "store", True)]
-
-
-def matvec_bytes(wd: str, rows: int, cols: int) -> int:
-    """Algorithmic HBM bytes of one launch: weights + scales (x and y are < 0.1 %)."""
-    n = rows * cols
-    if wd == "bf16":
-        return 2 * n
-    if wd == "int8":
-        return n + 4 * rows
-    return n // 2 + 2 * rows * (cols // 128)
-
-
-def bench_matvec(wd: str, name: str, rows: int, cols: int, ep: str, norm: bool, iters: int, torch,
-                 rpb: int = 0) -> dict:
-    """Median-free live timing: HIP events on torch's current stream around `iters` launches that
-    rotate over enough weight copies to exceed 1 GiB."""
-    from cudallm_amd import engine as E
-    dev = torch.device("cuda")
-    nbytes = matvec_bytes(wd, rows, cols)
-    copies = max(2, math.ceil((1 << 30) * 1.5 / nbytes))
-    g = torch.Generator(device=dev)
-    g.manual_seed(rows + cols)
-    ws, ss = [], []
-    for _ in range(copies):
-        if wd == "bf16":
-            ws.append((torch.randn(rows, cols, device=dev, generator=g) * 0.02).to(torch.bfloat16))
-            ss.append(None)
-        elif wd == "int8":
-            ws.append(torch.randint(-127, 128, (rows, cols), device=dev, dtype=torch.int8, generator=g))
-            ss.append(torch.rand(rows, device=dev, generator=g) * 0.01 + 0.005)
-        else:
-            ws.append(torch.randint(0, 256, (rows, cols // 2), device=dev, dtype=torch.uint8, generator=g))
-            ss.append((torch.rand(rows, cols // 128, device=dev, generator=g) * 0.01 + 0.005).half())
-    x = torch.randn(cols, device=dev)
-    nw = torch.rand(cols, device=dev) + 0.5
-    out_rows = rows // 2 if ep == "swiglu" else rows
-    y = torch.zeros(out_rows, device=dev)
-    stream = torch.cuda.current_stream()
-    sp = stream.cuda_stream
-
-    def launch(i):
-        w, s = ws[i % copies], ss[i % copies]
-        E.launch_matvec(wd, ep, rpb, w.data_ptr(), s.data_ptr() if s is not None else None, x.data_ptr(),
-                        nw.data_ptr() if norm else None, 1e-5, y.data_ptr(), rows, cols, sp)
-
-    for i in range(min(copies, 20)):
-        launch(i)
-    torch.cuda.synchronize()
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    for i in range(iters):
-        launch(i)
-    stop.record(stream)
-    stop.synchronize()
-    us = start.elapsed_time(stop) * 1e3 / iters
-    del ws, ss
-    torch.cuda.empty_cache()
-    return {"name": name, "wtype": wd, "rows": rows, "cols": cols, "epilogue": ep, "fuse_norm": norm,
-            "bytes": nbytes, "avg_us": us, "gbps": nbytes / us / 1e3, "frac_of_8tbs": nbytes / us / 1e3 / 8000.0,
-            "copies": copies}
 
 
 TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic.json"
@@ -261,17 +197,18 @@ def main() -> int:
             paths[wd].unlink()
 
     head_wd = "bf16" if "bf16" in dtypes else dtypes[0]
-    dom = bench_matvec(head_wd, "gate_up", 16384, 2048, "swiglu", True, 400, torch)
-    log(f"[bench] gate_up {head_wd} matvec: {dom['avg_us']:.2f} us, {dom['gbps']:.0f} GB/s")
+    dom = bench_matvec(head_wd, "gate_up", 16384, 2048, "swiglu", True, 400)
+    dom_gbps = dom["bytes"] / dom["avg_us"] / 1e3
+    log(f"[bench] gate_up {head_wd} matvec: {dom['avg_us']:.2f} us, {dom_gbps:.0f} GB/s")
     matvecs = []
     if not args.no_kernels:
         for wd in dtypes:
             per = {}
             for name, rows, cols, ep, norm in SHAPES:
-                r = bench_matvec(wd, name, rows, cols, ep, norm, 200 if name != "lm_head" else 50, torch)
+                r = bench_matvec(wd, name, rows, cols, ep, norm, 200 if name != "lm_head" else 50)
                 matvecs.append(r)
                 per[name] = r["avg_us"]
-            weighted = 16 * (per["qkv"] + per["wo"] + per["gate_up"] + per["down"]) + per["lm_head"]
+            weighted = weighted_us(per)
             matvecs.append({"name": "weighted_us", "wtype": wd, "us": weighted})
             log(f"[bench] {wd} matvec weighted 16*(qkv+wo+gate_up+down)+lm_head = {weighted:.1f} us")
 
@@ -299,7 +236,7 @@ def main() -> int:
                      "timing": "HIP events on the engine's stream around the timed steps",
                      "traffic_source": TRAFFIC_FILE.name},
         "matvec_roofline": {"kernel": f"matvec_fast<{head_wd}, SWIGLU, norm> gate_up 16384x2048 (standalone)",
-                            "achieved": round(dom["gbps"], 1), "frac": round(dom["frac_of_8tbs"], 4),
+                            "achieved": round(dom_gbps, 1), "frac": round(dom["frac_of_8tbs"], 4),
                             "bytes_per_launch": dom["bytes"], "avg_us": round(dom["avg_us"], 3)},
         "cpu_baseline": cpu,
         "decode": {wd: {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}

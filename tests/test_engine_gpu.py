@@ -270,3 +270,15 @@ def test_stalls_leave_results_bit_identical(wd, model_path, engine_runs, monkeyp
         print(f"[engine] {wd} stall {name} ({mask:#x}): bit-identical {same}", flush=True)
         np.testing.assert_array_equal(res, base["res"][:8], err_msg=f"stall {name}")
         np.testing.assert_array_equal(logits, base["logits"][:8], err_msg=f"stall {name}")
+
+
+@pytest.mark.parametrize("wd", ["bf16", "int8", "int4"])
+def test_eval_ppl_matches_oracle(wd, model_path, oracle_out):
+    """The perplexity caller (bench/eval_ppl.py:39-52) on one window: TOKENS[0] is BOS, so the oracle's logits after
+    TOKENS[p] score TOKENS[p + 1], exactly the engine's step(BOS), step(w[0]), ... protocol."""
+    from cudallm_amd import eval_ppl as P
+    got = P.eval_engine(model_path(wd), [TOKENS[1:]])[0]
+    lg, _ = oracle_out(wd)
+    want = float(np.mean([P.nll_from_logits(lg[p], TOKENS[p + 1]) for p in range(N_TOK - 1)]))
+    print(f"[engine] {wd} window NLL engine {got:.6f} oracle {want:.6f}", flush=True)
+    assert abs(got - want) < 5e-3
