@@ -196,6 +196,11 @@ def test_attention_large_scores_are_stable():
 def test_silu_mul():
     gu = (np.random.default_rng(14).standard_normal(2 * 8192) * 2).astype(np.float32)
     assert np.allclose(E.kernel_silu_mul(gu), K.silu_mul(gu), rtol=1e-5)
+    # the whole range where e^-g is a finite float, and past it (silu -> 0 below, -> g above)
+    g = np.concatenate([np.linspace(-87, 87, 8192), np.array([-200.0, -100.0, -88.5, 88.5, 100.0, 200.0] + [0.0] * 8186)])
+    gu = np.concatenate([g, np.ones_like(g)]).astype(np.float32)
+    got, want = E.kernel_silu_mul(gu), K.silu_mul(gu)
+    assert np.allclose(got, want, rtol=1e-5, atol=1e-30)
 
 
 VOCAB = 128256
