@@ -27,7 +27,7 @@ int device_cu_count() {
 
 int default_rpb(WType wt) {
     switch (wt) {
-        case WType::BF16: return 4;
+        case WType::BF16: return 2;
         case WType::INT8: return 4;
         case WType::INT4: return 4;
     }

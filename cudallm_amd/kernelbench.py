@@ -23,7 +23,7 @@ SHAPES = [("qkv", 3072, 2048, "store", True), ("wo", 2048, 2048, "add", False),
           ("lm_head", 128256, 2048, "store", True)]
 RPBS = (1, 2, 4, 8)
 # The library's choice when rpb = 0 (default_rpb in csrc/kernels/small.hip).
-DEFAULT_RPB = {"bf16": 4, "int8": 4, "int4": 4}
+DEFAULT_RPB = {"bf16": 2, "int8": 4, "int4": 4}
 PEAK_GBPS = 8000.0
 
 
