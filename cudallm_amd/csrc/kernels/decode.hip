@@ -1084,32 +1084,38 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
 #pragma unroll 1
             for (int h = gw; h < NH; h += NW) {
                 const uint64_t* pp = tpart + static_cast<size_t>(h) * NS * kPartStride;
-                float ms = -INFINITY, ls = 0.f;
+                const unsigned tag = tg + T_ATT_PART;
+                // One round trip for the first 16 splits: each lane's (m, l) and the o values all in flight at once.
+                uint64_t vm = static_cast<uint64_t>(tag) << 32, vl = vm;
                 if (lane < nsplit) {
-                    ms = wait1(pp + lane * kPartStride + HD, tg + T_ATT_PART, err);
-                    ls = wait1(pp + lane * kPartStride + HD + 1, tg + T_ATT_PART, err);
+                    vm = tload(pp + lane * kPartStride + HD);
+                    vl = tload(pp + lane * kPartStride + HD + 1);
                 }
-                const float M = wave_max(ms);
-                const float e = lane < nsplit ? expf(ms - M) : 0.f;
-                const float Lsum = wave_sum(ls * e);
-                float acc = 0.f;
+                float M = 0.f, e = 0.f, Lsum = 0.f, acc = 0.f;
 #pragma unroll 1
                 for (int sb = 0; sb < nsplit; sb += 16) {
                     uint64_t v[16];
 #pragma unroll
                     for (int k = 0; k < 16; ++k)
-                        v[k] = sb + k < nsplit ? tload(pp + (sb + k) * kPartStride + lane)
-                                               : (static_cast<uint64_t>(tg + T_ATT_PART) << 32);
+                        v[k] = sb + k < nsplit ? tload(pp + (sb + k) * kPartStride + lane) : static_cast<uint64_t>(tag) << 32;
                     unsigned spins = 0;
                     for (;;) {
-                        bool ok = true;
+                        bool ok = tagged(vm, tag) && tagged(vl, tag);
 #pragma unroll
-                        for (int k = 0; k < 16; ++k) ok = ok && tagged(v[k], tg + T_ATT_PART);
+                        for (int k = 0; k < 16; ++k) ok = ok && tagged(v[k], tag);
                         if (ok || give_up(spins, err)) break;
+                        if (!tagged(vm, tag)) vm = tload(pp + lane * kPartStride + HD);
+                        if (!tagged(vl, tag)) vl = tload(pp + lane * kPartStride + HD + 1);
 #pragma unroll
                         for (int k = 0; k < 16; ++k)
-                            if (sb + k < nsplit && !tagged(v[k], tg + T_ATT_PART))
-                                v[k] = tload(pp + (sb + k) * kPartStride + lane);
+                            if (sb + k < nsplit && !tagged(v[k], tag)) v[k] = tload(pp + (sb + k) * kPartStride + lane);
+                    }
+                    if (sb == 0) {
+                        const float ms = lane < nsplit ? tvalue(vm) : -INFINITY;
+                        const float ls = lane < nsplit ? tvalue(vl) : 0.f;
+                        M = wave_max(ms);
+                        e = lane < nsplit ? expf(ms - M) : 0.f;
+                        Lsum = wave_sum(ls * e);
                     }
 #pragma unroll
                     for (int k = 0; k < 16; ++k)
