@@ -155,6 +155,18 @@ __device__ __forceinline__ float wait1(const uint64_t* a, unsigned tag, unsigned
     while (!tagged(v, tag) && !give_up(spins, err)) v = tload(a);
     return tvalue(v);
 }
+// Wait for two tagged values (per lane) with both loads in flight: one round trip, not two.
+__device__ __forceinline__ void wait2(const uint64_t* a, const uint64_t* b, unsigned tag, unsigned* err, float& va,
+                                      float& vb) {
+    uint64_t x = tload(a), y = tload(b);
+    unsigned spins = 0;
+    while (!(tagged(x, tag) && tagged(y, tag)) && !give_up(spins, err)) {
+        if (!tagged(x, tag)) x = tload(a);
+        if (!tagged(y, tag)) y = tload(b);
+    }
+    va = tvalue(x);
+    vb = tvalue(y);
+}
 
 // Test hook: sleep about 13 us when the stall mask selects `bit` (and this workgroup, with kStallOdd).
 // The mask is a kernel argument, so the test is a scalar branch that normal runs never take.
@@ -984,9 +996,13 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
                 }
                 // q of the group's 4 heads (thread = head-in-group x dim) and, in the split holding this
                 // token, its k and v, rounded to fp16 exactly as the qkv phase wrote them to the cache.
-                qs[tid] = wait1(tqkv + (kvh * 4) * HD + tid, tg + T_QKV, err);
-                if (tid < 2 * HD && t0 + n - 1 == pos) {
-                    const float kv = wait1(tqkv + (tid < HD ? NH * HD : (NH + NKV) * HD - HD) + kvh * HD + tid, tg + T_QKV, err);
+                const uint64_t* qa = tqkv + (kvh * 4) * HD + tid;
+                const bool cur = tid < 2 * HD && t0 + n - 1 == pos;
+                float qv, kv;
+                wait2(qa, cur ? tqkv + (tid < HD ? NH * HD : (NH + NKV) * HD - HD) + kvh * HD + tid : qa, tg + T_QKV, err,
+                      qv, kv);
+                qs[tid] = qv;
+                if (cur) {
                     const int r = pos - t0;
                     if (tid < HD) {
                         Ks16[r * 2 * kKs + tid] = float_to_half_bits(kv);
@@ -1325,8 +1341,9 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
         float v = -INFINITY;
         int i = 0x7fffffff;
         for (int g = tid; g < G; g += kCT) {
-            const float gv = wait1(p.targ + 2 * g, base + T_ARG, err);
-            const int gi = __builtin_bit_cast(int, wait1(p.targ + 2 * g + 1, base + T_ARG, err));
+            float gv, gf;
+            wait2(p.targ + 2 * g, p.targ + 2 * g + 1, base + T_ARG, err, gv, gf);
+            const int gi = __builtin_bit_cast(int, gf);
             if (arg_better(gv, gi, v, i)) {
                 v = gv;
                 i = gi;
