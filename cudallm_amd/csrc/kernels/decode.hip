@@ -148,13 +148,6 @@ __device__ __forceinline__ bool give_up(unsigned& spins, unsigned* err) {
     return false;
 }
 
-// Wait for one tagged value (per lane).
-__device__ __forceinline__ float wait1(const uint64_t* a, unsigned tag, unsigned* err) {
-    uint64_t v = tload(a);
-    unsigned spins = 0;
-    while (!tagged(v, tag) && !give_up(spins, err)) v = tload(a);
-    return tvalue(v);
-}
 // Wait for two tagged values (per lane) with both loads in flight: one round trip, not two.
 __device__ __forceinline__ void wait2(const uint64_t* a, const uint64_t* b, unsigned tag, unsigned* err, float& va,
                                       float& vb) {
