@@ -493,12 +493,21 @@ __device__ __forceinline__ int dig_exponent(float m) {
     return 21 - ilogbf(m);
 }
 
+// The norm weights of columns 8 tid .. 8 tid + 7, loaded before the phase waits for its input so that the
+// digit prologue after the wait does not start a memory round trip of its own.
+struct Norm8 {
+    f32x4 g0, g1;
+};
+__device__ __forceinline__ Norm8 load_norm8(const float* g, int tid) {
+    return {*((global_f32x4*)g + 2 * tid), *((global_f32x4*)g + 2 * tid + 1)};
+}
+
 // Thread tid writes the digit words of columns 8 tid .. 8 tid + 7 (all 2048 by the compute group).
 template <WType WT>
-__device__ void make_digits(const float* x, const float* g, float inv, int e, uint32_t* tab, int tid) {
+__device__ void make_digits(const float* x, const Norm8& gn, float inv, int e, uint32_t* tab, int tid) {
     using D = Dig<WT>;
     const f32x4 x0 = reinterpret_cast<const f32x4*>(x)[2 * tid], x1 = reinterpret_cast<const f32x4*>(x)[2 * tid + 1];
-    const f32x4 g0 = *((global_f32x4*)g + 2 * tid), g1 = *((global_f32x4*)g + 2 * tid + 1);
+    const f32x4 g0 = gn.g0, g1 = gn.g1;
     uint32_t u[8];
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
@@ -555,12 +564,12 @@ __device__ __forceinline__ void load_digits(const uint32_t* tab, int lane, Dig<W
 // max |x g| and inv, and this thread's digit words into the table.  Returns 2^-e.  Callers follow
 // with a barrier, then load_digits().
 template <WType WT, typename SM>
-__device__ __forceinline__ float digits_prologue(SM& sm, float inv, const float* g, int tid, const float* x = nullptr) {
+__device__ __forceinline__ float digits_prologue(SM& sm, float inv, const Norm8& gn, int tid, const float* x = nullptr) {
     float m = 0.f;
 #pragma unroll
     for (int w = 0; w < kCW; ++w) m = fmaxf(m, sm.pmax[w]);
     const int e = dig_exponent(m * inv);
-    make_digits<WT>(x ? x : sm.xa, g, inv, e, reinterpret_cast<uint32_t*>(sm.big + kDigOff), tid);
+    make_digits<WT>(x ? x : sm.xa, gn, inv, e, reinterpret_cast<uint32_t*>(sm.big + kDigOff), tid);
     return ldexpf(1.f, -e);
 }
 
@@ -1166,11 +1175,12 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
             float dsc = 0.f;
             stall_at(p, kStallGateUp);
             if constexpr (kDig) {
+                const Norm8 gn = load_norm8(Lw.ffn_norm, tid);
                 fetch<H, true, 0, true>(txa, tg + T_XA, sm.xa, sm.part, err, tid, Lw.ffn_norm, sm.pmax);
                 cbar(sm.bar, ep, wave, lane, lbad);
                 stamp_in(p, l, 4, 0);
                 const float inv = rms_inv(sm.part, p.eps);
-                dsc = digits_prologue<WT>(sm, inv, Lw.ffn_norm, tid);
+                dsc = digits_prologue<WT>(sm, inv, gn, tid);
                 cbar(sm.bar, ep, wave, lane, lbad);
                 load_digits<WT>(reinterpret_cast<const uint32_t*>(sm.big + kDigOff), lane, dg);
             } else {
@@ -1240,10 +1250,11 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
         const unsigned tagfin = base + (NL - 1) * kTagStride + T_X;
         stall_at(p, kStallLmHead);
         if constexpr (kDig) {
+            const Norm8 gn = load_norm8(p.final_norm, tid);
             fetch<H, true, 0, true>(tfin, tagfin, sm.xin, sm.part, err, tid, p.final_norm, sm.pmax);
             cbar(sm.bar, ep, wave, lane, lbad);
             const float inv = rms_inv(sm.part, p.eps);
-            dsc = digits_prologue<WT>(sm, inv, p.final_norm, tid, sm.xin);
+            dsc = digits_prologue<WT>(sm, inv, gn, tid, sm.xin);
             cbar(sm.bar, ep, wave, lane, lbad);
             load_digits<WT>(reinterpret_cast<const uint32_t*>(sm.big + kDigOff), lane, dg);
         } else {
