@@ -75,9 +75,10 @@ struct RingCfg {
     static constexpr int SS = kQuant ? S : 1;                  // side-value slots
     static constexpr int LPR2 = Fmt<WT>::CPL;                  // lines per 2048-wide row
     static constexpr int LPR8 = INTER / Fmt<WT>::CPC / kWave;  // lines per 8192-wide row
-    // Lines in flight per loader wave (measured on MI355X: bf16 16, int8 12, int4 8; deeper queues
-    // also delay the small polling loads of the phase handoffs behind them).
-    static constexpr int NB = WT == WType::BF16 ? 16 : WT == WType::INT8 ? 12 : 8;
+    // Lines in flight per loader wave (measured on MI355X: bf16 16, int8 12, int4 16; deeper queues
+    // also delay the small polling loads of the phase handoffs behind them, which int4, whose rows are
+    // bound by the compute wave, can afford).
+    static constexpr int NB = WT == WType::BF16 ? 16 : WT == WType::INT8 ? 12 : 16;
 };
 
 template <WType WT>
@@ -788,6 +789,15 @@ __device__ __forceinline__ void stamp_attn(const DecodeParams& p, int l, bool fi
     if (l == 1 && first) stamp(p, kAttnSteps + k);
 }
 
+// SiLU g / (1 + e^-g) from the hardware base-2 exponential and reciprocal (each within about 1 ulp) instead
+// of expf's range reduction and an IEEE divide: about a third of the instructions, with a relative error of a
+// few 1e-7 for |g| < 20 and at most about 6e-6 where e^-g is a finite float.  Used by bf16 and int4 (-2.4 and
+// -7.9 us per step on MI355X); int8 keeps the exact form, which measured 10.8 us faster there, because a shorter
+// gate_up lets more of the loaders' streaming overlap the next handoffs.
+__device__ __forceinline__ float silu_hw(float g) {
+    return g * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-g * 1.4426950408889634f));  // log2(e)
+}
+
 // Drain this wave's outstanding global accesses before a row loop.  They are long complete by then
 // (earlier phases' stores); without it the compiler, which cannot tell the loop's first iteration
 // from the others, waits for them in every iteration before reusing their registers.
@@ -1211,7 +1221,7 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
                     uv = row_dot<WT>(ru, xr, xsum);
                 }
                 release(sm, cs, wave, lane);
-                if (lane == 0) tstore(tact + u, silu(gv) * uv, tg + T_ACT);
+                if (lane == 0) tstore(tact + u, (WT == WType::INT8 ? silu(gv) : silu_hw(gv)) * uv, tg + T_ACT);
             }
         }
         stamp(p, 1 + 6 * l + 4);
