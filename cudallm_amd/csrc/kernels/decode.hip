@@ -410,13 +410,14 @@ __device__ __forceinline__ int swz(int i) {
 // positions when SWZ > 0); with SQ, each wave also leaves the sum of squares of the values it
 // copied in part[wave].  Callers follow with cbar().
 //
-// With MXG, each wave also leaves max |x_i g_i| over the entries it copied in pmax[wave] (g: the
+// With MX = 1, each wave also leaves max |x_i g_i| over the entries it copied in pmax[wave] (g: the
 // norm weights, read while the wait runs), from which the fixed-point scale of the integer dot
-// products is derived.
-template <int N, bool SQ, int SWZ = 0, bool MXG = false>
+// products is derived; with MX = 2, max |x_i|.
+template <int N, bool SQ, int SWZ = 0, int MX = 0>
 __device__ void fetch(const uint64_t* src, unsigned tag, float* dst, float* part, unsigned* err, int tid,
                       const float* g = nullptr, float* pmax = nullptr) {
     constexpr int PT = N / kCT;
+    constexpr bool MXG = MX == 1;
     static_assert(N % kCT == 0, "fetch size");
     unsigned spins = 0;
     float gv[MXG ? PT : 1];
@@ -446,13 +447,14 @@ __device__ void fetch(const uint64_t* src, unsigned tag, float* dst, float* part
             dst[i] = x;
         }
         ss += x * x;
-        if constexpr (MXG) mx = fmaxf(mx, fabsf(x * gv[k]));
+        if constexpr (MX == 1) mx = fmaxf(mx, fabsf(x * gv[k]));
+        if constexpr (MX == 2) mx = fmaxf(mx, fabsf(x));
     }
     if constexpr (SQ) {
         ss = wave_sum(ss);
         if ((tid & (kWave - 1)) == 0) part[tid / kWave] = ss;
     }
-    if constexpr (MXG) {
+    if constexpr (MX != 0) {
         mx = wave_max(mx);
         if ((tid & (kWave - 1)) == 0) pmax[tid / kWave] = mx;
     }
@@ -684,6 +686,76 @@ __device__ __forceinline__ float row_dot_dig(const Row<WT>& r, const Dig<WT>& dg
         t = wave_sum(t * r.s);
         return t * sc;
     }
+}
+
+// ---- int4 down projection on digits ------------------------------------------------------------
+//
+// The 8192 SwiGLU outputs a get the same treatment as the normalised inputs of gate_up: one power-of-two
+// scale from max |a|, ai = rint(a 2^e), six signed base-16 digits packed like the weights.  Digit word
+// (k, m) holds digit k of columns 8m .. 8m + 7 at tab[k * 1024 + m]; a down row's line c gives lane l the
+// columns 2048 c + 32 l .. + 31, i.e. words m = 256 c + 4 l + i.
+constexpr int kDownWords = INTER / 8;  // digit words per digit
+
+// Thread tid builds the digit words of column groups m = tid + kCT j (j < 4) from the natural-order inputs in
+// LDS.  Callers read (this) before a barrier and write the table after it, over the same LDS.
+__device__ __forceinline__ void down_digits(const float* a, int e, int tid, uint32_t (&dw)[4][6]) {
+    static_assert(INTER / 8 / kCT == 4, "four column groups per thread");
+    static_assert(6 * kDownWords <= kBig, "the digit table fits where the inputs were");
+    constexpr uint32_t C = 0x888888u;
+#pragma unroll
+    for (int j = 0; j < INTER / 8 / kCT; ++j) {
+        const int m = tid + kCT * j;
+        const f32x4 x0 = reinterpret_cast<const f32x4*>(a)[2 * m], x1 = reinterpret_cast<const f32x4*>(a)[2 * m + 1];
+        uint32_t u[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const float xc = c < 4 ? x0[c] : x1[c - 4];
+            u[c] = (static_cast<uint32_t>(static_cast<int>(rintf(ldexpf(xc, e)))) + C) ^ C;
+        }
+#pragma unroll
+        for (int k = 0; k < 6; ++k) {
+            uint32_t w = 0;
+#pragma unroll
+            for (int b = 0; b < 8; ++b) w |= ((u[b] >> (4 * k)) & 0xfu) << (4 * b);
+            dw[j][k] = w;
+        }
+    }
+}
+
+// One int4 down row (4 ring lines) against the digit table; `sc` = 2^-e.  Per line and lane: the six digit
+// dot products recombined exactly, times the lane's group scale.
+__device__ __forceinline__ float down_dot_dig4(Smem<WType::INT4>& sm, Cons& cs, const uint32_t* tab, float sc, int wave,
+                                               int lane, bool& lbad) {
+    using C = RingCfg<WType::INT4>;
+    static_assert(C::LPR8 == 4, "int4 down rows are 4 lines");
+    ring_wait(cs.k + 4, cs.cfull, &sm.full[wave], lbad);
+    u32x4 w[4];
+    float gs[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        w[g] = sm.ring[wave][(cs.k + g) % C::S][lane];
+        gs[g] = sm.side[wave][(cs.k + g) % C::S][lane];
+    }
+    float s = 0.f;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const uint32_t* t = tab + (g * kWave + lane) * 4;
+        u32x4 d[6];
+#pragma unroll
+        for (int k = 0; k < 6; ++k) d[k] = *reinterpret_cast<const u32x4*>(t + k * kDownWords);
+        int a[6] = {0, 0, 0, 0, 0, 0};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int wq = static_cast<int>(w[g][i] ^ 0x88888888u);
+#pragma unroll
+            for (int k = 0; k < 6; ++k) a[k] = __builtin_amdgcn_sdot8(wq, static_cast<int>(d[k][i]), a[k], false);
+        }
+        const int p0 = a[0] + 16 * a[1], p1 = a[2] + 16 * a[3], p2 = a[4] + 16 * a[5];
+        s = fmaf(fmaf(static_cast<float>(p2), 65536.f, static_cast<float>(p0 + 256 * p1)), gs[g], s);
+    }
+    cs.k += 4;
+    release(sm, cs, wave, lane);
+    return wave_sum(s) * sc;
 }
 
 // Per-chunk sums of the lane's down-projection inputs (the bias correction of quantised chunks);
@@ -1230,15 +1302,43 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
         renew();
         {
             stall_at(p, kStallDown);
-            fetch<INTER, false, F::CPC>(tact, tg + T_ACT, sm.big, sm.part, err, tid);
-            cbar(sm.bar, ep, wave, lane, lbad);
-            stamp_in(p, l, 5, 0);
-            DownSums<WT> dsum;
-            down_sums<WT>(sm.big, lane, dsum);
+            [[maybe_unused]] DownSums<WT> dsum;
+            [[maybe_unused]] float dsc = 0.f;
+            if constexpr (WT == WType::INT4) {
+                // Digits, as in gate_up: natural-order inputs, their max, the digit words in registers, a
+                // barrier (every thread has read its inputs), then the table over the same LDS.
+                fetch<INTER, false, 0, 2>(tact, tg + T_ACT, sm.big, sm.part, err, tid, nullptr, sm.pmax);
+                cbar(sm.bar, ep, wave, lane, lbad);
+                stamp_in(p, l, 5, 0);
+                float m = 0.f;
+#pragma unroll
+                for (int w = 0; w < kCW; ++w) m = fmaxf(m, sm.pmax[w]);
+                const int e = dig_exponent(m);
+                dsc = ldexpf(1.f, -e);
+                uint32_t dw[4][6];
+                down_digits(sm.big, e, tid, dw);
+                cbar(sm.bar, ep, wave, lane, lbad);
+                uint32_t* tab = reinterpret_cast<uint32_t*>(sm.big);
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int k = 0; k < 6; ++k) tab[k * kDownWords + tid + kCT * j] = dw[j][k];
+                cbar(sm.bar, ep, wave, lane, lbad);
+            } else {
+                fetch<INTER, false, F::CPC>(tact, tg + T_ACT, sm.big, sm.part, err, tid);
+                cbar(sm.bar, ep, wave, lane, lbad);
+                stamp_in(p, l, 5, 0);
+                down_sums<WT>(sm.big, lane, dsum);
+            }
             drain();
 #pragma unroll 1
             for (int r = gw; r < H; r += NW) {
-                const float d = down_dot<WT>(sm, cs, sm.big, dsum, wave, lane, lbad);
+                float d;
+                if constexpr (WT == WType::INT4) {
+                    d = down_dot_dig4(sm, cs, reinterpret_cast<const uint32_t*>(sm.big), dsc, wave, lane, lbad);
+                } else {
+                    d = down_dot<WT>(sm, cs, sm.big, dsum, wave, lane, lbad);
+                }
                 if (lane == 0) {
                     const float xn = sm.xa[r] + d;
                     tstore(txo + r, xn, tg + T_X);
