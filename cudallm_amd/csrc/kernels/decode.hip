@@ -758,6 +758,67 @@ __device__ __forceinline__ float down_dot_dig4(Smem<WType::INT4>& sm, Cons& cs, 
     return wave_sum(s) * sc;
 }
 
+// int8: three signed base-256 digits; digit word (k, m) holds digit k of columns 4m .. 4m + 3 at
+// tab[k * 2048 + m], so a down row's line c gives lane l the words m = 256 c + 4 l + i.
+__device__ __forceinline__ void down_digits8(const float* a, int e, int tid, uint32_t (&dw)[4][6]) {
+    constexpr uint32_t C = 0x808080u;
+#pragma unroll
+    for (int j = 0; j < INTER / 8 / kCT; ++j) {
+        const int m = tid + kCT * j;
+        const f32x4 x0 = reinterpret_cast<const f32x4*>(a)[2 * m], x1 = reinterpret_cast<const f32x4*>(a)[2 * m + 1];
+        uint32_t u[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const float xc = c < 4 ? x0[c] : x1[c - 4];
+            u[c] = (static_cast<uint32_t>(static_cast<int>(rintf(ldexpf(xc, e)))) + C) ^ C;
+        }
+#pragma unroll
+        for (int k = 0; k < 3; ++k)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                uint32_t w = 0;
+#pragma unroll
+                for (int b = 0; b < 4; ++b) w |= ((u[4 * h + b] >> (8 * k)) & 0xffu) << (8 * b);
+                dw[j][2 * k + h] = w;
+            }
+    }
+}
+
+// One int8 down row (8 ring lines, four at a time) against the digit table; `sc` = 2^-e.  The digit dot
+// products stay integer over the whole row; the row scale is applied once.
+__device__ __forceinline__ float down_dot_dig8(Smem<WType::INT8>& sm, Cons& cs, const uint32_t* tab, float sc, int wave,
+                                               int lane, bool& lbad) {
+    using C = RingCfg<WType::INT8>;
+    static_assert(C::LPR8 == 8, "int8 down rows are 8 lines");
+    int a0 = 0, a1 = 0, a2 = 0;
+    float rs = 1.f;
+#pragma unroll
+    for (int c0 = 0; c0 < 8; c0 += 4) {
+        ring_wait(cs.k + 4, cs.cfull, &sm.full[wave], lbad);
+        u32x4 w[4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) w[g] = sm.ring[wave][(cs.k + g) % C::S][lane];
+        rs = sm.side[wave][cs.k % C::S][lane];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const uint32_t* t = tab + ((c0 + g) * kWave + lane) * 4;
+            const u32x4 d0 = *reinterpret_cast<const u32x4*>(t), d1 = *reinterpret_cast<const u32x4*>(t + 2 * kDownWords),
+                        d2 = *reinterpret_cast<const u32x4*>(t + 4 * kDownWords);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int wi = static_cast<int>(w[g][i]);
+                a0 = __builtin_amdgcn_sdot4(wi, static_cast<int>(d0[i]), a0, false);
+                a1 = __builtin_amdgcn_sdot4(wi, static_cast<int>(d1[i]), a1, false);
+                a2 = __builtin_amdgcn_sdot4(wi, static_cast<int>(d2[i]), a2, false);
+            }
+        }
+        cs.k += 4;
+        release(sm, cs, wave, lane);
+    }
+    const float t = fmaf(fmaf(static_cast<float>(a2), 256.f, static_cast<float>(a1)), 256.f, static_cast<float>(a0));
+    return wave_sum(t) * sc * rs;
+}
+
 // Per-chunk sums of the lane's down-projection inputs (the bias correction of quantised chunks);
 // the same for every row, so computed once per phase.
 template <WType WT>
@@ -1304,7 +1365,7 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
             stall_at(p, kStallDown);
             [[maybe_unused]] DownSums<WT> dsum;
             [[maybe_unused]] float dsc = 0.f;
-            if constexpr (WT == WType::INT4) {
+            if constexpr (kDig) {
                 // Digits, as in gate_up: natural-order inputs, their max, the digit words in registers, a
                 // barrier (every thread has read its inputs), then the table over the same LDS.
                 fetch<INTER, false, 0, 2>(tact, tg + T_ACT, sm.big, sm.part, err, tid, nullptr, sm.pmax);
@@ -1316,13 +1377,23 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
                 const int e = dig_exponent(m);
                 dsc = ldexpf(1.f, -e);
                 uint32_t dw[4][6];
-                down_digits(sm.big, e, tid, dw);
+                if constexpr (WT == WType::INT4) {
+                    down_digits(sm.big, e, tid, dw);
+                } else {
+                    down_digits8(sm.big, e, tid, dw);
+                }
                 cbar(sm.bar, ep, wave, lane, lbad);
                 uint32_t* tab = reinterpret_cast<uint32_t*>(sm.big);
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
 #pragma unroll
-                    for (int k = 0; k < 6; ++k) tab[k * kDownWords + tid + kCT * j] = dw[j][k];
+                    for (int k = 0; k < 6; ++k) {
+                        if constexpr (WT == WType::INT4) {
+                            tab[k * kDownWords + tid + kCT * j] = dw[j][k];
+                        } else {  // digit k / 2, word 2 m + k % 2 of the 4-column words
+                            tab[(k / 2) * 2 * kDownWords + 2 * (tid + kCT * j) + k % 2] = dw[j][k];
+                        }
+                    }
                 cbar(sm.bar, ep, wave, lane, lbad);
             } else {
                 fetch<INTER, false, F::CPC>(tact, tg + T_ACT, sm.big, sm.part, err, tid);
@@ -1336,6 +1407,8 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
                 float d;
                 if constexpr (WT == WType::INT4) {
                     d = down_dot_dig4(sm, cs, reinterpret_cast<const uint32_t*>(sm.big), dsc, wave, lane, lbad);
+                } else if constexpr (WT == WType::INT8) {
+                    d = down_dot_dig8(sm, cs, reinterpret_cast<const uint32_t*>(sm.big), dsc, wave, lane, lbad);
                 } else {
                     d = down_dot<WT>(sm, cs, sm.big, dsum, wave, lane, lbad);
                 }
