@@ -6,8 +6,8 @@ A "step" is one batch-1 decode step (one token) of a seeded random-init Llama-3.
 16 layers, hidden 2048, FFN 8192, vocab 128256, GQA 32/8, tied embeddings, weights N(0, 0.02)
 (bf16 master; int8 per-row and int4 group-128 files quantised from it).  Per weight type: a 16-token
 seeded prompt, W untimed warm-up decode steps, then K greedy decode steps timed with the device
-drained on both sides; each step is one replay of the captured hipGraph with the token fed back on
-the device (no host sync inside the timed region, as reference src/tools/cudallm_bench.cpp:64-80).
+drained on both sides; each step is one launch of the persistent decode kernel with the token fed
+back on the device (no host sync inside the timed region, as reference src/tools/cudallm_bench.cpp:64-80).
 
 Printed last, on one line: the JSON record.  ``value`` is bf16 decode tok/s; ``decode`` holds all
 three weight types; ``roofline`` is the dominant kernel, the persistent decode kernel (one launch
@@ -61,7 +61,7 @@ def bench_decode(path, wd: str, steps: int, warmup: int, torch) -> dict:
         for _ in range(warmup):
             eng.step_async(None)
         torch.cuda.synchronize()
-        # HIP events on the engine's own stream, where each step is one graph replay of the decode kernel.
+        # HIP events on the engine's own stream, where each step is one launch of the decode kernel.
         es = torch.cuda.ExternalStream(eng.stream)
         ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         t0 = time.perf_counter()
@@ -226,7 +226,7 @@ def main() -> int:
         "scaling": "weak", "vs_baseline": None, "dtype": head_wd,
         "data": "synthetic: seeded random-init Llama-3.2-1B-shaped weights N(0,0.02), bf16 master",
         "config": {"workload": f"batch-1 greedy decode, {head_wd} weights, 16-token prompt + {args.warmup} warm-up "
-                               f"+ {args.steps} timed steps, hipGraph replay (BASELINE config 5)",
+                               f"+ {args.steps} timed steps, one kernel launch per step (BASELINE config 5)",
                    "model": "llama-3.2-1b-shaped (random init)", "global_batch": 1,
                    "seq_len": PROMPT + args.warmup + args.steps, "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "hbm", "achieved": round(head["kernel_gbps"], 1), "peak": 8000.0, "unit": "GB/s",
