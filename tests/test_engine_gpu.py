@@ -135,10 +135,12 @@ def test_reset_determinism(cfg, engine_runs):
     np.testing.assert_array_equal(run["rerun"], run["logits"][:4])
 
 
-@pytest.mark.parametrize("wd", ["bf16", "int8", "int4"])
-def test_graph_replay_equals_eager(wd, engine_runs):
-    np.testing.assert_array_equal(engine_runs((wd, "opt", "opt", 1, 1))["logits"],
-                                  engine_runs((wd, "opt", "opt", 1, 0))["logits"])
+@pytest.mark.parametrize("wd,fuse", [("bf16", 1), ("int8", 1), ("int4", 1), ("bf16", 0)])
+def test_graph_replay_equals_eager(wd, fuse, engine_runs):
+    """cuda_graph on vs off, bit for bit: for fuse=0 the multi-kernel step is captured once and replayed; for fuse=1
+    the persistent kernel is launched directly either way, through step() vs step_debug()."""
+    np.testing.assert_array_equal(engine_runs((wd, "opt", "opt", fuse, 1))["logits"],
+                                  engine_runs((wd, "opt", "opt", fuse, 0))["logits"])
 
 
 @pytest.mark.parametrize("wd", ["bf16", "int8", "int4"])
