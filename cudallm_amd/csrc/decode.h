@@ -76,6 +76,9 @@ enum : unsigned {
 constexpr int kStampSlots = 128;
 
 constexpr int kDecodeThreads = 512;  // 4 compute waves + 4 loader waves
+// Grid bounds of the decode kernel: each compute wave keeps the residual inputs of its wo/down rows in
+// LDS for at most 8 rows (2048 rows over >= 64 x 4 waves).
+constexpr int kDecodeMinGrid = 64, kDecodeMaxGrid = 4096;
 
 // Enqueue one decode step (one launch).  `grid` workgroups must all be co-resident.
 void launch_decode(WType wt, const DecodeParams& p, int grid, hipStream_t s);

@@ -66,12 +66,12 @@ Engine::Engine(const std::string& path, const EngineOptions& opts) : opts_(opts)
                      o_ai = cv.take<int>(kArgmaxParts), o_tok = cv.take<int>(1), o_pos = cv.take<int>(1),
                      o_k = cv.take<uint16_t>(L * KV * S * D), o_v = cv.take<uint16_t>(L * KV * S * D);
         // Persistent decode kernel: fused + opt options, contexts up to 8192 (one split per lane
-        // in the LSE merge), and one co-resident workgroup per CU.  CUDALLM_PERSISTENT=0 selects
+        // in the LSE merge), and one co-resident workgroup per CU (64 to 4096 CUs).  CUDALLM_PERSISTENT=0 selects
         // the kernel-per-op graph instead (for comparisons).
         const char* env = std::getenv("CUDALLM_PERSISTENT");
         const bool want = opts_.fuse && opts_.matvec == 1 && opts_.attn == 1 && S <= 8192 && !(env && !std::strcmp(env, "0"));
         grid_ = device_cu_count();
-        persistent_ = want && grid_ <= 4096 && decode_max_grid(c.wt) >= grid_;
+        persistent_ = want && grid_ >= kDecodeMinGrid && grid_ <= kDecodeMaxGrid && decode_max_grid(c.wt) >= grid_;
         const size_t QKV = (NH + 2 * KV) * D;
         const size_t o_tx = cv.take<uint64_t>((L + 1) * H), o_txa = cv.take<uint64_t>(L * H),
                      o_tqkv = cv.take<uint64_t>(L * QKV), o_tatt = cv.take<uint64_t>(L * NH * D),

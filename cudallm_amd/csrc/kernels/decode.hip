@@ -66,12 +66,27 @@ constexpr int kAttnV = kAttnChunk * kKs, kAttnP = kAttnV + kAttnChunk * HD / 2, 
 constexpr int kDigOff = INTER, kDigWordsMax = 3 * 512;
 constexpr int kBig = kAttnQ + 4 * HD > kDigOff + kDigWordsMax ? kAttnQ + 4 * HD : kDigOff + kDigWordsMax;
 static_assert(kBig >= INTER, "big holds the down-projection input");
+// Phase inputs live in big too, which leaves the LDS to the rings.  bf16 (whose swizzled down input spans
+// all 8192 floats) puts every input at big + 0, each overwrite behind a barrier or a carrive/cwait pair.
+// The quantised weights have room to spare: the layer input (qkv; lm_head's final-norm input) gets a
+// region of its own past the digit table and gate_up's input sits at big + H beside wo's, so none of
+// those fetches waits for another wave.
+template <WType WT>
+constexpr int kXin = WT == WType::BF16 ? 0 : kBig;
+template <WType WT>
+constexpr int kXgu = WT == WType::BF16 ? 0 : H;
+template <WType WT>
+constexpr int kBigOf = WT == WType::BF16 ? kBig : kBig + H;
+// Rows of wo and down per compute wave (r = gw, gw + NW, ...) at the smallest grid the kernel takes: the
+// residual inputs at those rows are all a wave keeps of the layer input and of the residual after attention.
+constexpr int kRPW = 8;
+static_assert(kDecodeMinGrid * kCW * kRPW >= H, "residual rows per wave");
 
 // Ring geometry per weight type.
 template <WType WT>
 struct RingCfg {
     static constexpr bool kQuant = WT != WType::BF16;
-    static constexpr int S = kQuant ? 20 : 24;                 // 1 KiB slots per compute wave
+    static constexpr int S = kQuant ? 20 : 30;                 // 1 KiB slots per compute wave (bf16: what fits)
     static constexpr int SS = kQuant ? S : 1;                  // side-value slots
     static constexpr int LPR2 = Fmt<WT>::CPL;                  // lines per 2048-wide row
     static constexpr int LPR8 = INTER / Fmt<WT>::CPC / kWave;  // lines per 8192-wide row
@@ -85,9 +100,9 @@ template <WType WT>
 struct Smem {
     u32x4 ring[kCW][RingCfg<WT>::S][kWave];
     float side[kCW][RingCfg<WT>::SS][kWave];
-    float xin[H];     // layer input (residual stream)
-    float xa[H];      // residual after attention
-    float big[kBig];  // attention tiles | attention output | SwiGLU output
+    float big[kBigOf<WT>];  // phase inputs | attention tiles | SwiGLU output | digit tables
+    float xres[kCW * kRPW];  // layer input at the wave's wo rows
+    float ares[kCW * kRPW];  // residual after attention at the wave's down rows (the same rows)
     float rope_c[HD / 2], rope_s[HD / 2];
     float part[kCW];
     float pmax[kCW];  // per-wave max |x g| of the last fetch with MXG
@@ -211,6 +226,26 @@ __device__ __forceinline__ void cbar(unsigned* bar, unsigned& ep, int wave, int 
 #pragma unroll
         for (int w = 0; w < kCW; ++w) lo = min(lo, __hip_atomic_load(bar + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
         if (lo >= ep || lds_give_up(spins, lbad)) break;
+    }
+    asm volatile("" ::: "memory");
+}
+
+// cbar in two halves: carrive() publishes the wave's next epoch (it has finished reading what the
+// barrier protects) and returns it; cwait(e) waits until every compute wave has published e.  Waves
+// announce early and wait only where they are about to overwrite.
+__device__ __forceinline__ unsigned carrive(unsigned* bar, unsigned& ep, int wave, int lane) {
+    ++ep;
+    asm volatile("" ::: "memory");
+    if (lane == 0) __hip_atomic_store(bar + wave, ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    return ep;
+}
+__device__ __forceinline__ void cwait(unsigned* bar, unsigned e, bool& lbad) {
+    unsigned spins = 0;
+    for (;;) {
+        unsigned lo = ~0u;
+#pragma unroll
+        for (int w = 0; w < kCW; ++w) lo = min(lo, __hip_atomic_load(bar + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+        if (lo >= e || lds_give_up(spins, lbad)) break;
     }
     asm volatile("" ::: "memory");
 }
@@ -572,7 +607,7 @@ __device__ __forceinline__ float digits_prologue(SM& sm, float inv, const Norm8&
 #pragma unroll
     for (int w = 0; w < kCW; ++w) m = fmaxf(m, sm.pmax[w]);
     const int e = dig_exponent(m * inv);
-    make_digits<WT>(x ? x : sm.xa, gn, inv, e, reinterpret_cast<uint32_t*>(sm.big + kDigOff), tid);
+    make_digits<WT>(x ? x : sm.big, gn, inv, e, reinterpret_cast<uint32_t*>(sm.big + kDigOff), tid);
     return ldexpf(1.f, -e);
 }
 
@@ -1019,6 +1054,7 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
     };
     renew();
     unsigned ep = 0;     // compute-barrier epoch
+    unsigned ep_in = 0;  // epoch of the last carrive(): every wave has read the phase input in big
     bool lbad = false;   // an in-workgroup wait overran (reported at the end)
     Cons cs;
 
@@ -1027,7 +1063,7 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
         float ss = 0.f;
         for (int j = tid; j < H; j += kCT) {
             const float x = embed<WT>(p.emb, p.emb_s, tok, j);
-            sm.xin[j] = x;
+            sm.big[kXin<WT> + j] = x;
             ss += x * x;
         }
         ss = wave_sum(ss);
@@ -1041,7 +1077,7 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
     }
     cbar(sm.bar, ep, wave, lane, lbad);
     if (p.residuals && blockIdx.x == 0)
-        for (int j = tid; j < H; j += kCT) *glob(p.residuals + j) = sm.xin[j];
+        for (int j = tid; j < H; j += kCT) *glob(p.residuals + j) = sm.big[kXin<WT> + j];
 
 #pragma unroll 1
     for (int l = 0; l < NL; ++l) {
@@ -1061,13 +1097,16 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
             load_norm<WT>(Lw.attn_norm, lane, nw);
             stall_at(p, kStallQkv);
             if (l > 0) {
-                fetch<H, true>(p.tx + static_cast<size_t>(l) * H, tg - kTagStride + T_X, sm.xin, sm.part, err, tid);
+                if constexpr (!kDig) cbar(sm.bar, ep, wave, lane, lbad);  // every wave is done with the down input
+                fetch<H, true>(p.tx + static_cast<size_t>(l) * H, tg - kTagStride + T_X, sm.big + kXin<WT>, sm.part, err, tid);
                 cbar(sm.bar, ep, wave, lane, lbad);
             }
             stamp_in(p, l, 0, 0);
             const float inv = rms_inv(sm.part, p.eps);
             float xr[NX], xsum;
-            lane_inputs<WT, true>(sm.xin, &nw, inv, xr, xsum, lane);
+            lane_inputs<WT, true>(sm.big + kXin<WT>, &nw, inv, xr, xsum, lane);
+            if (lane < kRPW && gw + lane * NW < H) sm.xres[wave * kRPW + lane] = sm.big[kXin<WT> + gw + lane * NW];
+            ep_in = carrive(sm.bar, ep, wave, lane);  // the attention tiles may now overwrite the input
             stamp_in(p, l, 0, 1);
             drain();
 #pragma unroll 1
@@ -1130,6 +1169,7 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
                             vt[k] = load_stream(Vg + static_cast<size_t>(t0 + r) * HD + c * 8);
                         }
                     }
+                    if (!kDig && first) cwait(sm.bar, ep_in, lbad);  // every wave has read the qkv input
 #pragma unroll
                     for (int k = 0; k < kTile; ++k) {
                         const int idx = tid + k * kCT, r = idx / 8, c = idx % 8;
@@ -1291,20 +1331,27 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
         renew();
         {
             stall_at(p, kStallWo);
+            if constexpr (!kDig) cwait(sm.bar, ep_in, lbad);  // every wave has read the qkv input (as above)
             fetch<H, false>(tatt, tg + T_ATT, sm.big, sm.part, err, tid);
             cbar(sm.bar, ep, wave, lane, lbad);
             stamp_in(p, l, 3, 0);
             float xr[NX], xsum;
             lane_inputs<WT, false>(sm.big, nullptr, 1.f, xr, xsum, lane);
+            ep_in = carrive(sm.bar, ep, wave, lane);  // gate_up's input may now overwrite this one
             stamp_in(p, l, 3, 1);
             drain();
+            int k = wave * kRPW;
 #pragma unroll 1
-            for (int r = gw; r < H; r += NW) {
+            for (int r = gw; r < H; r += NW, ++k) {
                 Row<WT> rw;
                 take_row<WT>(sm, cs, wave, lane, lbad, rw);
                 const float d = row_dot<WT>(rw, xr, xsum);
                 release(sm, cs, wave, lane);
-                if (lane == 0) tstore(txa + r, sm.xin[r] + d, tg + T_XA);
+                if (lane == 0) {
+                    const float xa = sm.xres[k] + d;
+                    tstore(txa + r, xa, tg + T_XA);
+                    sm.ares[k] = xa;
+                }
             }
         }
         stamp(p, 1 + 6 * l + 3);
@@ -1319,20 +1366,22 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
             stall_at(p, kStallGateUp);
             if constexpr (kDig) {
                 const Norm8 gn = load_norm8(Lw.ffn_norm, tid);
-                fetch<H, true, 0, true>(txa, tg + T_XA, sm.xa, sm.part, err, tid, Lw.ffn_norm, sm.pmax);
+                fetch<H, true, 0, true>(txa, tg + T_XA, sm.big + kXgu<WT>, sm.part, err, tid, Lw.ffn_norm, sm.pmax);
                 cbar(sm.bar, ep, wave, lane, lbad);
                 stamp_in(p, l, 4, 0);
                 const float inv = rms_inv(sm.part, p.eps);
-                dsc = digits_prologue<WT>(sm, inv, gn, tid);
+                dsc = digits_prologue<WT>(sm, inv, gn, tid, sm.big + kXgu<WT>);
                 cbar(sm.bar, ep, wave, lane, lbad);
                 load_digits<WT>(reinterpret_cast<const uint32_t*>(sm.big + kDigOff), lane, dg);
             } else {
                 load_norm<WT>(Lw.ffn_norm, lane, nw);
-                fetch<H, true>(txa, tg + T_XA, sm.xa, sm.part, err, tid);
+                cwait(sm.bar, ep_in, lbad);  // every wave has read wo's input
+                fetch<H, true>(txa, tg + T_XA, sm.big, sm.part, err, tid);
                 cbar(sm.bar, ep, wave, lane, lbad);
                 stamp_in(p, l, 4, 0);
                 const float inv = rms_inv(sm.part, p.eps);
-                lane_inputs<WT, true>(sm.xa, &nw, inv, xr, xsum, lane);
+                lane_inputs<WT, true>(sm.big, &nw, inv, xr, xsum, lane);
+                ep_in = carrive(sm.bar, ep, wave, lane);  // the down projection's input may now overwrite it
             }
             stamp_in(p, l, 4, 1);
             drain();
@@ -1396,14 +1445,16 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
                     }
                 cbar(sm.bar, ep, wave, lane, lbad);
             } else {
+                cwait(sm.bar, ep_in, lbad);  // every wave has read gate_up's input
                 fetch<INTER, false, F::CPC>(tact, tg + T_ACT, sm.big, sm.part, err, tid);
                 cbar(sm.bar, ep, wave, lane, lbad);
                 stamp_in(p, l, 5, 0);
                 down_sums<WT>(sm.big, lane, dsum);
             }
             drain();
+            int k = wave * kRPW;
 #pragma unroll 1
-            for (int r = gw; r < H; r += NW) {
+            for (int r = gw; r < H; r += NW, ++k) {
                 float d;
                 if constexpr (WT == WType::INT4) {
                     d = down_dot_dig4(sm, cs, reinterpret_cast<const uint32_t*>(sm.big), dsc, wave, lane, lbad);
@@ -1413,7 +1464,7 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
                     d = down_dot<WT>(sm, cs, sm.big, dsum, wave, lane, lbad);
                 }
                 if (lane == 0) {
-                    const float xn = sm.xa[r] + d;
+                    const float xn = sm.ares[k] + d;
                     tstore(txo + r, xn, tg + T_X);
                     if (p.residuals) *glob(p.residuals + static_cast<size_t>(l + 1) * H + r) = xn;
                 }
@@ -1434,18 +1485,19 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
         stall_at(p, kStallLmHead);
         if constexpr (kDig) {
             const Norm8 gn = load_norm8(p.final_norm, tid);
-            fetch<H, true, 0, true>(tfin, tagfin, sm.xin, sm.part, err, tid, p.final_norm, sm.pmax);
+            fetch<H, true, 0, true>(tfin, tagfin, sm.big + kXin<WT>, sm.part, err, tid, p.final_norm, sm.pmax);
             cbar(sm.bar, ep, wave, lane, lbad);
             const float inv = rms_inv(sm.part, p.eps);
-            dsc = digits_prologue<WT>(sm, inv, gn, tid, sm.xin);
+            dsc = digits_prologue<WT>(sm, inv, gn, tid, sm.big + kXin<WT>);
             cbar(sm.bar, ep, wave, lane, lbad);
             load_digits<WT>(reinterpret_cast<const uint32_t*>(sm.big + kDigOff), lane, dg);
         } else {
             load_norm<WT>(p.final_norm, lane, nw);
-            fetch<H, true>(tfin, tagfin, sm.xin, sm.part, err, tid);
+            cbar(sm.bar, ep, wave, lane, lbad);  // every wave is done with the down projection's input
+            fetch<H, true>(tfin, tagfin, sm.big, sm.part, err, tid);
             cbar(sm.bar, ep, wave, lane, lbad);
             const float inv = rms_inv(sm.part, p.eps);
-            lane_inputs<WT, true>(sm.xin, &nw, inv, xr, xsum, lane);
+            lane_inputs<WT, true>(sm.big, &nw, inv, xr, xsum, lane);
         }
         float bv = -INFINITY;
         int bi = 0x7fffffff;
@@ -1576,7 +1628,7 @@ int decode_max_grid(WType wt) {
 }
 
 void launch_decode(WType wt, const DecodeParams& p, int grid, hipStream_t s) {
-    CLLM_REQUIRE(grid > 0 && grid <= 4096, "decode: bad grid");
+    CLLM_REQUIRE(grid >= kDecodeMinGrid && grid <= kDecodeMaxGrid, "decode: grid must be 64..4096 workgroups");
     CLLM_REQUIRE(p.max_seq > 0 && p.max_seq % kAttnChunk == 0 && p.max_seq <= 64 * kAttnChunk,
                  "decode: max_seq must be a multiple of 128 and at most 8192");
     switch (wt) {
