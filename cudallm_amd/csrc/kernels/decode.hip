@@ -90,10 +90,9 @@ struct RingCfg {
     static constexpr int SS = kQuant ? S : 1;                  // side-value slots
     static constexpr int LPR2 = Fmt<WT>::CPL;                  // lines per 2048-wide row
     static constexpr int LPR8 = INTER / Fmt<WT>::CPC / kWave;  // lines per 8192-wide row
-    // Lines in flight per loader wave (measured on MI355X: bf16 16, int8 12, int4 16; deeper queues
-    // also delay the small polling loads of the phase handoffs behind them, which int4, whose rows are
-    // bound by the compute wave, can afford).
-    static constexpr int NB = WT == WType::BF16 ? 16 : WT == WType::INT8 ? 12 : 16;
+    // Lines in flight per loader wave (16, measured on MI355X against 12: deeper queues also delay the
+    // small polling loads of the phase handoffs behind them; 12 and 16 are within a few us).
+    static constexpr int NB = 16;
 };
 
 template <WType WT>
@@ -1211,17 +1210,17 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
                     for (int k = 0; k < 2; ++k) {
                         const int j = lane + kWave * k;
                         if (j < n) {
-                            float dot = 0.f;
+                            float dd[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                             for (int i = 0; i < HD / 8; ++i) {
                                 const u32x4 kk = *reinterpret_cast<const u32x4*>(Ks + j * kKs + 4 * i);
 #pragma unroll
                                 for (int e = 0; e < 4; ++e) {
-                                    dot = fmaf(half_bits_to_float(static_cast<uint16_t>(kk[e])), qv[2 * i + e / 2][2 * (e % 2)], dot);
-                                    dot = fmaf(half_bits_to_float(static_cast<uint16_t>(kk[e] >> 16)), qv[2 * i + e / 2][2 * (e % 2) + 1], dot);
+                                    dd[e] = fmaf(half_bits_to_float(static_cast<uint16_t>(kk[e])), qv[2 * i + e / 2][2 * (e % 2)], dd[e]);
+                                    dd[e] = fmaf(half_bits_to_float(static_cast<uint16_t>(kk[e] >> 16)), qv[2 * i + e / 2][2 * (e % 2) + 1], dd[e]);
                                 }
                             }
-                            s[k] = 0.125f * dot;
+                            s[k] = 0.125f * ((dd[0] + dd[1]) + (dd[2] + dd[3]));  // 4 chains: 2.5-5.5 us per step
                         } else {
                             s[k] = -INFINITY;
                         }
