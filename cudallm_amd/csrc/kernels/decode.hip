@@ -153,13 +153,14 @@ __device__ __forceinline__ bool failed(unsigned* err) {
 __device__ __forceinline__ void fail(unsigned* err) {
     __hip_atomic_fetch_or(glob(err), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-// True when a wait must stop: it ran out of polls, or another wave already failed.
+// True when a wait must stop: it ran out of polls, or another wave already failed.  Polls are not
+// spaced by s_sleep: each already takes a memory round trip, and without the sleep int4 measured
+// 3.8 us per step faster on MI355X (bf16 and int8 within 1.5 us).
 __device__ __forceinline__ bool give_up(unsigned& spins, unsigned* err) {
     if (++spins >= kSpinCap || ((spins & 255u) == 0 && failed(err))) {
         fail(err);
         return true;
     }
-    __builtin_amdgcn_s_sleep(1);
     return false;
 }
 
