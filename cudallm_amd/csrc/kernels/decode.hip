@@ -961,9 +961,9 @@ __device__ __forceinline__ void stamp_attn(const DecodeParams& p, int l, bool fi
 
 // SiLU g / (1 + e^-g) from the hardware base-2 exponential and reciprocal (each within about 1 ulp) instead
 // of expf's range reduction and an IEEE divide: about a third of the instructions, with a relative error of a
-// few 1e-7 for |g| < 20 and at most about 6e-6 where e^-g is a finite float.  Used by bf16 and int4 (-2.4 and
-// -7.9 us per step on MI355X); int8 keeps the exact form, which measured 10.8 us faster there, because a shorter
-// gate_up lets more of the loaders' streaming overlap the next handoffs.
+// few 1e-7 for |g| < 20 and at most about 6e-6 where e^-g is a finite float.  Measured on MI355X against the
+// exact form: bf16 -2.4, int4 -7.9, int8 -4 us per step (int8 was +10.8 before the layer inputs moved out of
+// the LDS, when a shorter gate_up let more streaming overlap the next handoffs).
 __device__ __forceinline__ float silu_hw(float g) {
     return g * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-g * 1.4426950408889634f));  // log2(e)
 }
@@ -1405,7 +1405,7 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
                     uv = row_dot<WT>(ru, xr, xsum);
                 }
                 release(sm, cs, wave, lane);
-                if (lane == 0) tstore(tact + u, (WT == WType::INT8 ? silu(gv) : silu_hw(gv)) * uv, tg + T_ACT);
+                if (lane == 0) tstore(tact + u, silu_hw(gv) * uv, tg + T_ACT);
             }
         }
         stamp(p, 1 + 6 * l + 4);
