@@ -67,6 +67,8 @@ enum : unsigned {
     kStallLmHead = 1u << 5,
     kStallLoader = 1u << 6,
     kStallOdd = 1u << 7,
+    kStallInputs = 1u << 8,  // after a phase's input barrier, before the waves read the input from LDS
+    kStallWave0 = 1u << 9,   // only compute wave 0 of a selected workgroup sleeps (skew inside the workgroup)
 };
 
 // Timestamp slots per workgroup: 0 = start, 1 + 6 l + k = end of phase k of layer l

@@ -180,7 +180,8 @@ __device__ __forceinline__ void wait2(const uint64_t* a, const uint64_t* b, unsi
 // Test hook: sleep about 13 us when the stall mask selects `bit` (and this workgroup, with kStallOdd).
 // The mask is a kernel argument, so the test is a scalar branch that normal runs never take.
 __device__ __forceinline__ void stall_at(const DecodeParams& p, unsigned bit) {
-    if ((p.stall & bit) && (!(p.stall & kStallOdd) || (blockIdx.x & 1))) {
+    if ((p.stall & bit) && (!(p.stall & kStallOdd) || (blockIdx.x & 1)) &&
+        (!(p.stall & kStallWave0) || threadIdx.x < kWave)) {
 #pragma unroll 1
         for (int i = 0; i < 4; ++i) __builtin_amdgcn_s_sleep(127);
     }
@@ -1104,6 +1105,7 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
                 cbar(sm.bar, ep, wave, lane, lbad);
             }
             stamp_in(p, l, 0, 0);
+            stall_at(p, kStallInputs);
             const float inv = rms_inv(sm.part, p.eps);
             float xr[NX], xsum;
             lane_inputs<WT, true>(sm.big + kXin<WT>, &nw, inv, xr, xsum, lane);
@@ -1337,6 +1339,7 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
             fetch<H, false>(tatt, tg + T_ATT, sm.big, sm.part, err, tid);
             cbar(sm.bar, ep, wave, lane, lbad);
             stamp_in(p, l, 3, 0);
+            stall_at(p, kStallInputs);
             float xr[NX], xsum;
             lane_inputs<WT, false>(sm.big, nullptr, 1.f, xr, xsum, lane);
             ep_in = carrive(sm.bar, ep, wave, lane);  // gate_up's input may now overwrite this one
@@ -1371,6 +1374,7 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
                 fetch<H, true, 0, true>(txa, tg + T_XA, sm.big + kXgu<WT>, sm.part, err, tid, Lw.ffn_norm, sm.pmax);
                 cbar(sm.bar, ep, wave, lane, lbad);
                 stamp_in(p, l, 4, 0);
+                stall_at(p, kStallInputs);
                 const float inv = rms_inv(sm.part, p.eps);
                 dsc = digits_prologue<WT>(sm, inv, gn, tid, sm.big + kXgu<WT>);
                 cbar(sm.bar, ep, wave, lane, lbad);
@@ -1381,6 +1385,7 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
                 fetch<H, true>(txa, tg + T_XA, sm.big, sm.part, err, tid);
                 cbar(sm.bar, ep, wave, lane, lbad);
                 stamp_in(p, l, 4, 0);
+                stall_at(p, kStallInputs);
                 const float inv = rms_inv(sm.part, p.eps);
                 lane_inputs<WT, true>(sm.big, &nw, inv, xr, xsum, lane);
                 ep_in = carrive(sm.bar, ep, wave, lane);  // the down projection's input may now overwrite it
@@ -1451,6 +1456,7 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
                 fetch<INTER, false, F::CPC>(tact, tg + T_ACT, sm.big, sm.part, err, tid);
                 cbar(sm.bar, ep, wave, lane, lbad);
                 stamp_in(p, l, 5, 0);
+                stall_at(p, kStallInputs);
                 down_sums<WT>(sm.big, lane, dsum);
             }
             drain();

@@ -251,7 +251,11 @@ def test_persistent_long_context_matches_multikernel(wd, model_path, monkeypatch
 # Stall masks (bits of DecodeParams::stall in cudallm_amd/csrc/decode.h): before the down projection's
 # input wait (the loader then runs a layer ahead), the loaders at their segment switches, odd
 # workgroups only (skew between workgroups), and every point at once.
-STALLS = {"down": 0x10, "loader": 0x40, "odd_down": 0x90, "all": 0x7F, "odd_all": 0xFF}
+# Bits: 0x01..0x20 phase starts (qkv, attention, wo, gate_up, down, lm_head), 0x40 loader segment switch,
+# 0x80 odd workgroups only, 0x100 between a phase's input barrier and its input reads, 0x200 compute wave 0
+# only (the other waves of its workgroup run ahead into the next phase's writes of the shared LDS buffer).
+STALLS = {"down": 0x10, "loader": 0x40, "odd_down": 0x90, "all": 0x7F, "odd_all": 0xFF,
+          "w0_inputs": 0x300, "w0_odd_inputs": 0x380}
 
 
 @pytest.mark.parametrize("wd", ["bf16", "int8", "int4"])
