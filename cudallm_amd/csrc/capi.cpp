@@ -1,22 +1,29 @@
-// The C ABI (include/cudallm/cudallm.h).  Behaviour of each entry point follows reference
-// src/capi/cudallm_capi.cpp:84-316: every call is guarded, exceptions become error codes plus a
-// thread-local message, test hooks are synchronous and allocate per call.
+// The C ABI of include/cudallm/cudallm.h: names, signatures, struct layouts and error codes of the
+// reference interface (include/cudallm/cudallm.h:8-56, src/capi/cudallm_capi.cpp:84-316).
+//
+// Structure of this file:
+//  * abi_entry() runs an entry point's body; a C++ exception never crosses the ABI, it becomes one of
+//    the CUDALLM_* codes (chosen by the exception's type) and a thread-local message that names the
+//    entry point.
+//  * Test hooks stage their host operands through one device allocation per call (HookStaging), run
+//    the kernel on the null stream, synchronise, and copy the outputs back.
 #include "cudallm/cudallm.h"
 
 #include <cstring>
+#include <memory>
 #include <string>
+#include <vector>
 
 #include "engine.h"
 
 struct cudallm_engine {
-    cllm::Engine* impl;
+    std::unique_ptr<cllm::Engine> impl;
 };
 
 namespace cllm {
 
 [[noreturn]] void throw_hip(hipError_t err, const char* expr, const char* file, int line) {
-    throw DeviceError(std::string("HIP error at ") + file + ":" + std::to_string(line) + ": " + expr + ": " +
-                      hipGetErrorString(err));
+    throw DeviceError(std::string(hipGetErrorString(err)) + " (" + expr + " at " + file + ":" + std::to_string(line) + ")");
 }
 
 const char* wtype_name(WType w) {
@@ -32,90 +39,110 @@ const char* wtype_name(WType w) {
 
 namespace {
 
-thread_local std::string g_last_error;
+thread_local std::string t_message;
 
-int code_of(const std::exception& e) {
-    if (dynamic_cast<const cllm::ArgError*>(&e)) return CUDALLM_ERR_INVALID_ARG;
-    if (dynamic_cast<const cllm::FormatError*>(&e)) return CUDALLM_ERR_FORMAT;
-    if (dynamic_cast<const cllm::IoError*>(&e)) return CUDALLM_ERR_IO;
-    if (dynamic_cast<const cllm::DeviceError*>(&e)) return CUDALLM_ERR_CUDA;
-    if (dynamic_cast<const cllm::StateError*>(&e)) return CUDALLM_ERR_STATE;
-    return CUDALLM_ERR_INTERNAL;
+int record(int code, const char* entry, const char* what) {
+    t_message = std::string(entry) + ": " + what;
+    return code;
 }
 
-template <typename F>
-int guarded(F&& f) {
+template <typename Body>
+int abi_entry(const char* entry, Body&& body) noexcept {
     try {
-        f();
+        body();
         return CUDALLM_OK;
-    } catch (const std::exception& e) {
-        g_last_error = e.what();
-        return code_of(e);
+    } catch (const cllm::ArgError& e) {
+        return record(CUDALLM_ERR_INVALID_ARG, entry, e.what());
+    } catch (const cllm::IoError& e) {
+        return record(CUDALLM_ERR_IO, entry, e.what());
+    } catch (const cllm::FormatError& e) {
+        return record(CUDALLM_ERR_FORMAT, entry, e.what());
+    } catch (const cllm::DeviceError& e) {
+        return record(CUDALLM_ERR_CUDA, entry, e.what());
+    } catch (const cllm::StateError& e) {
+        return record(CUDALLM_ERR_STATE, entry, e.what());
+    } catch (const std::exception& e) {  // SequenceFull and logic errors: INTERNAL, as the reference reports them
+        return record(CUDALLM_ERR_INTERNAL, entry, e.what());
     } catch (...) {
-        g_last_error = "unknown exception";
-        return CUDALLM_ERR_INTERNAL;
+        return record(CUDALLM_ERR_INTERNAL, entry, "unrecognised exception");
     }
 }
 
-// Device buffer owned by one test-hook call.
-class DevBuf {
-public:
-    explicit DevBuf(size_t bytes) : n_(bytes) {
-        if (bytes) CLLM_HIP(hipMalloc(&p_, bytes));
-    }
-    ~DevBuf() {
-        if (p_) (void)hipFree(p_);
-    }
-    DevBuf(const DevBuf&) = delete;
-    DevBuf& operator=(const DevBuf&) = delete;
-    template <typename T>
-    T* as() const {
-        return static_cast<T*>(p_);
-    }
-    void put(const void* src) {
-        if (n_) CLLM_HIP(hipMemcpy(p_, src, n_, hipMemcpyHostToDevice));
-    }
-    void get(void* dst) const {
-        if (n_) CLLM_HIP(hipMemcpy(dst, p_, n_, hipMemcpyDeviceToHost));
-    }
+cllm::Engine& engine_of(cudallm_engine* e) {
+    if (!e || !e->impl) throw cllm::ArgError("null engine handle");
+    return *e->impl;
+}
 
-private:
-    void* p_ = nullptr;
-    size_t n_;
-};
-
-void finish() {
-    CLLM_HIP(hipGetLastError());
-    CLLM_HIP(hipDeviceSynchronize());
+void need(bool ok, const char* why) {
+    if (!ok) throw cllm::ArgError(why);
 }
 
 cllm::WType weight_type(int code) {
-    CLLM_REQUIRE(code == 1 || code == 3 || code == 4, "weight_dtype must be 1 (bf16), 3 (int8) or 4 (int4)");
+    need(code == 1 || code == 3 || code == 4, "weight_dtype must be 1 (bf16), 3 (int8) or 4 (int4)");
     return static_cast<cllm::WType>(code);
 }
+
+// Device memory for one hook call: operands are declared first (host source or sink and size), then
+// one allocation is made and the inputs are uploaded; finish() waits for the kernels and copies the
+// outputs back.  Freed when the call returns, on every path.
+class HookStaging {
+public:
+    enum Dir { In, Out, InOut, Scratch };
+    int add(const void* host, size_t bytes, Dir dir) {
+        slots_.push_back({const_cast<void*>(host), bytes, dir, total_});
+        total_ += (bytes + 255) / 256 * 256;
+        return static_cast<int>(slots_.size()) - 1;
+    }
+    void upload() {
+        if (total_) CLLM_HIP(hipMalloc(&dev_, total_));
+        for (const Slot& s : slots_)
+            if ((s.dir == In || s.dir == InOut) && s.bytes)
+                CLLM_HIP(hipMemcpy(at(s), s.host, s.bytes, hipMemcpyHostToDevice));
+    }
+    template <typename T>
+    T* dev(int slot) const {
+        return slots_[slot].bytes ? static_cast<T*>(at(slots_[slot])) : nullptr;
+    }
+    void finish() {
+        CLLM_HIP(hipGetLastError());
+        CLLM_HIP(hipDeviceSynchronize());
+        for (const Slot& s : slots_)
+            if ((s.dir == Out || s.dir == InOut) && s.bytes)
+                CLLM_HIP(hipMemcpy(s.host, at(s), s.bytes, hipMemcpyDeviceToHost));
+    }
+    ~HookStaging() {
+        if (dev_) (void)hipFree(dev_);
+    }
+
+private:
+    struct Slot {
+        void* host;
+        size_t bytes;
+        Dir dir;
+        size_t offset;
+    };
+    void* at(const Slot& s) const { return static_cast<char*>(dev_) + s.offset; }
+    std::vector<Slot> slots_;
+    size_t total_ = 0;
+    void* dev_ = nullptr;
+};
 
 }  // namespace
 
 extern "C" {
 
-const char* cudallm_last_error(void) { return g_last_error.c_str(); }
+const char* cudallm_last_error(void) { return t_message.c_str(); }
 
 void cudallm_default_options(cudallm_options* out) {
-    if (!out) return;
-    out->matvec_impl = 1;
-    out->attn_impl = 1;
-    out->fuse = 1;
-    out->cuda_graph = 1;
-    out->max_seq_len = 0;
-    out->matvec_rpb = 0;
+    if (out) *out = cudallm_options{1, 1, 1, 1, 0, 0};  // opt, opt, fused, graph, file max_seq_len, default rpb
 }
 
 int cudallm_create(const char* path, const cudallm_options* opts, cudallm_engine** out) {
-    return guarded([&] {
-        CLLM_REQUIRE(path && opts && out, "cudallm_create: null argument");
-        *out = nullptr;
-        CLLM_REQUIRE(opts->matvec_impl == 0 || opts->matvec_impl == 1, "matvec_impl must be 0 or 1");
-        CLLM_REQUIRE(opts->attn_impl == 0 || opts->attn_impl == 1, "attn_impl must be 0 or 1");
+    if (out) *out = nullptr;
+    return abi_entry("cudallm_create", [&] {
+        need(path && opts && out, "path, options and output handle are required");
+        need(opts->matvec_impl == 0 || opts->matvec_impl == 1, "matvec_impl must be 0 or 1");
+        need(opts->attn_impl == 0 || opts->attn_impl == 1, "attn_impl must be 0 or 1");
         cllm::EngineOptions o;
         o.matvec = opts->matvec_impl;
         o.attn = opts->attn_impl;
@@ -123,243 +150,230 @@ int cudallm_create(const char* path, const cudallm_options* opts, cudallm_engine
         o.graph = opts->cuda_graph != 0;
         o.max_seq_len = opts->max_seq_len;
         o.matvec_rpb = opts->matvec_rpb;
-        auto* e = new cudallm_engine{nullptr};
-        try {
-            e->impl = new cllm::Engine(path, o);
-        } catch (...) {
-            delete e;
-            throw;
-        }
-        *out = e;
+        auto handle = std::make_unique<cudallm_engine>();
+        handle->impl = std::make_unique<cllm::Engine>(path, o);
+        *out = handle.release();
     });
 }
 
-void cudallm_destroy(cudallm_engine* e) {
-    if (!e) return;
-    delete e->impl;
-    delete e;
-}
+void cudallm_destroy(cudallm_engine* e) { delete e; }
 
 int cudallm_get_config(cudallm_engine* e, cudallm_config_info* out) {
-    return guarded([&] {
-        CLLM_REQUIRE(e && e->impl && out, "cudallm_get_config: null argument");
-        const cllm::ModelConfig& c = e->impl->config();
-        out->weight_dtype = static_cast<int>(c.wt);
-        out->hidden = c.hidden;
-        out->inter = c.inter;
-        out->n_layers = c.n_layers;
-        out->n_heads = c.n_heads;
-        out->n_kv_heads = c.n_kv_heads;
-        out->head_dim = c.head_dim;
-        out->vocab = c.vocab;
-        out->max_seq_len = e->impl->max_seq();
-        out->group_size = c.group_size;
-        out->rms_eps = c.rms_eps;
-        out->weight_bytes = e->impl->weight_bytes();
+    return abi_entry("cudallm_get_config", [&] {
+        cllm::Engine& eng = engine_of(e);
+        need(out, "output struct is required");
+        const cllm::ModelConfig& c = eng.config();
+        cudallm_config_info info{};
+        info.weight_dtype = static_cast<int>(c.wt);
+        info.hidden = c.hidden;
+        info.inter = c.inter;
+        info.n_layers = c.n_layers;
+        info.n_heads = c.n_heads;
+        info.n_kv_heads = c.n_kv_heads;
+        info.head_dim = c.head_dim;
+        info.vocab = c.vocab;
+        info.max_seq_len = eng.max_seq();  // the engine's (option) value, not necessarily the file's
+        info.group_size = c.group_size;
+        info.rms_eps = c.rms_eps;
+        info.weight_bytes = eng.weight_bytes();
+        *out = info;
     });
 }
 
 int cudallm_reset(cudallm_engine* e) {
-    return guarded([&] {
-        CLLM_REQUIRE(e && e->impl, "cudallm_reset: null engine");
-        e->impl->reset();
-    });
+    return abi_entry("cudallm_reset", [&] { engine_of(e).reset(); });
 }
 
 int cudallm_pos(cudallm_engine* e) {
     if (!e || !e->impl) {
-        g_last_error = "cudallm_pos: null engine";
+        record(CUDALLM_ERR_INVALID_ARG, "cudallm_pos", "null engine handle");
         return -1;
     }
     return e->impl->pos();
 }
 
 int cudallm_step(cudallm_engine* e, int token, float* logits_out, int* next_token_out) {
-    return guarded([&] {
-        CLLM_REQUIRE(e && e->impl, "cudallm_step: null engine");
-        CLLM_REQUIRE(token >= -1, "cudallm_step: token must be >= -1");
-        e->impl->step(token, logits_out, next_token_out);
-    });
+    return abi_entry("cudallm_step", [&] { engine_of(e).step(token, logits_out, next_token_out); });
 }
 
 int cudallm_step_debug(cudallm_engine* e, int token, float* residuals_out, float* logits_out, int* next_token_out) {
-    return guarded([&] {
-        CLLM_REQUIRE(e && e->impl, "cudallm_step_debug: null engine");
-        CLLM_REQUIRE(token >= -1, "cudallm_step_debug: token must be >= -1");
-        CLLM_REQUIRE(residuals_out, "cudallm_step_debug: residuals_out is null");
-        e->impl->step_debug(token, residuals_out, logits_out, next_token_out);
-    });
+    return abi_entry("cudallm_step_debug",
+                     [&] { engine_of(e).step_debug(token, residuals_out, logits_out, next_token_out); });
 }
 
 int cudallm_step_profile(cudallm_engine* e, int token, unsigned long long* stamps_out, long long capacity,
                          int* grid_out) {
-    return guarded([&] {
-        CLLM_REQUIRE(e && e->impl && grid_out, "cudallm_step_profile: null argument");
-        CLLM_REQUIRE(token >= -1, "cudallm_step_profile: token must be >= -1");
-        *grid_out = e->impl->step_profile(token, stamps_out, static_cast<long>(capacity));
+    return abi_entry("cudallm_step_profile", [&] {
+        cllm::Engine& eng = engine_of(e);
+        need(grid_out, "grid_out is required");
+        *grid_out = eng.step_profile(token, stamps_out, static_cast<long>(capacity));
+    });
+}
+
+int cudallm_step_trace(cudallm_engine* e, int token, float* trace_out, long long capacity, float* logits_out,
+                       int* next_token_out) {
+    return abi_entry("cudallm_step_trace", [&] {
+        engine_of(e).step_trace(token, trace_out, static_cast<long>(capacity), logits_out, next_token_out);
     });
 }
 
 int cudallm_get_stream(cudallm_engine* e, void** stream_out) {
-    return guarded([&] {
-        CLLM_REQUIRE(e && e->impl && stream_out, "cudallm_get_stream: null argument");
-        *stream_out = e->impl->stream();
+    if (stream_out) *stream_out = nullptr;
+    return abi_entry("cudallm_get_stream", [&] {
+        cllm::Engine& eng = engine_of(e);
+        need(stream_out, "stream_out is required");
+        *stream_out = eng.stream();
     });
 }
 
 int cudallm_kernel_matvec(int impl, int weight_dtype, int epilogue, int fuse_norm, int rpb, const void* w,
                           unsigned long long w_bytes, const void* scales, unsigned long long scales_bytes,
                           const float* x, const float* norm_w, float eps, float* y, int rows, int cols) {
-    return guarded([&] {
-        CLLM_REQUIRE(w && x && y && w_bytes > 0, "cudallm_kernel_matvec: null argument");
-        CLLM_REQUIRE(rows > 0 && cols > 0, "cudallm_kernel_matvec: bad shape");
-        CLLM_REQUIRE(impl == 0 || impl == 1, "cudallm_kernel_matvec: impl must be 0 or 1");
-        CLLM_REQUIRE(epilogue >= 0 && epilogue <= 2, "cudallm_kernel_matvec: bad epilogue");
+    return abi_entry("cudallm_kernel_matvec", [&] {
         const cllm::WType wt = weight_type(weight_dtype);
+        need(impl == 0 || impl == 1, "impl must be 0 (naive) or 1 (opt)");
+        need(epilogue == 0 || epilogue == 1 || epilogue == 2, "epilogue must be 0 (STORE), 1 (ADD) or 2 (SWIGLU)");
+        need(rows > 0 && cols > 0, "rows and cols must be positive");
+        need(w && x && y, "w, x and y are required");
+        need(rpb == 0 || rpb == 1 || rpb == 2 || rpb == 4 || rpb == 8, "rpb must be 0, 1, 2, 4 or 8");
         const auto ep = static_cast<cllm::Epilogue>(epilogue);
-        if (impl == 0)
-            CLLM_REQUIRE(wt == cllm::WType::BF16 && ep == cllm::Epilogue::STORE && !fuse_norm,
-                         "cudallm_kernel_matvec: naive requires bf16, STORE and no fused norm");
-        if (fuse_norm) CLLM_REQUIRE(norm_w, "cudallm_kernel_matvec: fuse_norm needs norm_w");
-        if (wt != cllm::WType::BF16)
-            CLLM_REQUIRE(scales && scales_bytes > 0, "cudallm_kernel_matvec: quantized weights need scales");
-        CLLM_REQUIRE(rpb == 0 || rpb == 1 || rpb == 2 || rpb == 4 || rpb == 8,
-                     "cudallm_kernel_matvec: rpb must be 0, 1, 2, 4 or 8");
-        // Buffer sizes must cover the shape: the kernels never read past what the caller passed.
-        const uint64_t n = static_cast<uint64_t>(rows) * cols;
-        const uint64_t need_w = wt == cllm::WType::BF16 ? 2 * n : wt == cllm::WType::INT8 ? n : n / 2;
-        CLLM_REQUIRE(w_bytes >= need_w, "cudallm_kernel_matvec: w_bytes is smaller than rows x cols needs");
-        if (wt == cllm::WType::INT8)
-            CLLM_REQUIRE(scales_bytes >= 4ull * rows, "cudallm_kernel_matvec: scales_bytes too small");
+        need(impl == 1 || (wt == cllm::WType::BF16 && ep == cllm::Epilogue::STORE && !fuse_norm),
+             "the naive kernel takes bf16 weights, the STORE epilogue and no fused norm only");
+        need(!fuse_norm || norm_w, "fuse_norm is set but norm_w is null");
+        const uint64_t n = static_cast<uint64_t>(rows) * static_cast<uint64_t>(cols);
+        // What the shape needs of each buffer; the kernels never read past what the caller passed.
+        uint64_t w_need = 2 * n, s_need = 0;
+        if (wt == cllm::WType::INT8) w_need = n, s_need = 4ull * rows;
         if (wt == cllm::WType::INT4) {
-            CLLM_REQUIRE(cols % 128 == 0, "cudallm_kernel_matvec: int4 needs cols % 128 == 0");
-            CLLM_REQUIRE(scales_bytes >= 2ull * rows * (cols / 128), "cudallm_kernel_matvec: scales_bytes too small");
+            need(cols % 128 == 0, "int4 weights need cols to be a multiple of 128");
+            w_need = n / 2, s_need = 2ull * rows * (cols / 128);
         }
-        const int out_rows = ep == cllm::Epilogue::SWIGLU ? rows / 2 : rows;
+        need(w_bytes >= w_need, "w_bytes does not cover rows x cols");
+        need(s_need == 0 || (scales && scales_bytes >= s_need),
+             "quantised weights need scales (scales_bytes covering every row or group)");
+        const int y_rows = ep == cllm::Epilogue::SWIGLU ? rows / 2 : rows;
 
-        DevBuf dw(w_bytes), ds(scales ? scales_bytes : 0), dx(sizeof(float) * cols),
-            dn(fuse_norm ? sizeof(float) * cols : 0), dy(sizeof(float) * out_rows);
-        dw.put(w);
-        if (scales) ds.put(scales);
-        dx.put(x);
-        if (fuse_norm) dn.put(norm_w);
-        dy.put(y);
-        cllm::MatvecArgs a{dw.as<void>(), scales ? ds.as<void>() : nullptr, dx.as<float>(),
-                           fuse_norm ? dn.as<float>() : nullptr, eps, dy.as<float>(), rows, cols};
+        HookStaging st;
+        const int sw = st.add(w, w_bytes, HookStaging::In);
+        const int ss = st.add(scales, scales ? scales_bytes : 0, HookStaging::In);
+        const int sx = st.add(x, sizeof(float) * cols, HookStaging::In);
+        const int sn = st.add(norm_w, fuse_norm ? sizeof(float) * cols : 0, HookStaging::In);
+        const int sy = st.add(y, sizeof(float) * y_rows, HookStaging::InOut);  // ADD reads y
+        st.upload();
+        const cllm::MatvecArgs a{st.dev<void>(sw), st.dev<void>(ss), st.dev<float>(sx), st.dev<float>(sn), eps,
+                                 st.dev<float>(sy), rows, cols};
         if (impl == 0)
             cllm::launch_matvec_naive(a, nullptr);
         else
             cllm::launch_matvec(wt, ep, a, rpb ? rpb : cllm::default_rpb(wt), nullptr);
-        finish();
-        dy.get(y);
+        st.finish();
     });
 }
 
 int cudallm_kernel_rmsnorm(const float* x, const float* w, float eps, float* y, int n) {
-    return guarded([&] {
-        CLLM_REQUIRE(x && w && y && n > 0, "cudallm_kernel_rmsnorm: bad argument");
-        const size_t bytes = sizeof(float) * n;
-        DevBuf dx(bytes), dw(bytes), dy(bytes);
-        dx.put(x);
-        dw.put(w);
-        cllm::launch_rmsnorm(dx.as<float>(), dw.as<float>(), eps, dy.as<float>(), n, nullptr);
-        finish();
-        dy.get(y);
+    return abi_entry("cudallm_kernel_rmsnorm", [&] {
+        need(x && w && y && n > 0, "x, w and y are required and n must be positive");
+        HookStaging st;
+        const size_t b = sizeof(float) * n;
+        const int sx = st.add(x, b, HookStaging::In), sw = st.add(w, b, HookStaging::In), sy = st.add(y, b, HookStaging::Out);
+        st.upload();
+        cllm::launch_rmsnorm(st.dev<float>(sx), st.dev<float>(sw), eps, st.dev<float>(sy), n, nullptr);
+        st.finish();
     });
 }
 
 int cudallm_kernel_rope_kv(int fused, float* qkv, const float* inv_freq, int pos, unsigned short* k_cache,
                            unsigned short* v_cache, int nh, int nkv, int hd, int max_seq) {
-    return guarded([&] {
-        CLLM_REQUIRE(qkv && inv_freq && k_cache && v_cache, "cudallm_kernel_rope_kv: null argument");
-        CLLM_REQUIRE(nh > 0 && nkv > 0 && hd > 0 && hd % 2 == 0 && max_seq > 0 && pos >= 0 && pos < max_seq,
-                     "cudallm_kernel_rope_kv: bad dimensions");
-        const size_t qkv_bytes = sizeof(float) * (nh + 2 * nkv) * hd;
-        const size_t cache_bytes = sizeof(uint16_t) * static_cast<size_t>(nkv) * max_seq * hd;
-        DevBuf dq(qkv_bytes), dinv(sizeof(float) * (hd / 2)), dk(cache_bytes), dv(cache_bytes), dpos(sizeof(int));
-        dq.put(qkv);
-        dinv.put(inv_freq);
-        dk.put(k_cache);
-        dv.put(v_cache);
-        dpos.put(&pos);
+    return abi_entry("cudallm_kernel_rope_kv", [&] {
+        need(qkv && inv_freq && k_cache && v_cache, "qkv, inv_freq and both caches are required");
+        need(nh > 0 && nkv > 0 && hd > 0 && hd % 2 == 0 && max_seq > 0, "head counts, an even head_dim and max_seq must be positive");
+        need(pos >= 0 && pos < max_seq, "pos must lie in [0, max_seq)");
+        const size_t cache = sizeof(uint16_t) * static_cast<size_t>(nkv) * max_seq * hd;
+        HookStaging st;
+        const int sq = st.add(qkv, sizeof(float) * (nh + 2 * nkv) * hd, HookStaging::InOut);
+        const int si = st.add(inv_freq, sizeof(float) * (hd / 2), HookStaging::In);
+        const int sk = st.add(k_cache, cache, HookStaging::InOut), sv = st.add(v_cache, cache, HookStaging::InOut);
+        const int sp = st.add(&pos, sizeof(int), HookStaging::In);
+        st.upload();
+        float* q = st.dev<float>(sq);
+        uint16_t *kc = st.dev<uint16_t>(sk), *vc = st.dev<uint16_t>(sv);
+        const int* dpos = st.dev<int>(sp);
         if (fused) {
-            cllm::launch_rope_kv_fused(dq.as<float>(), dinv.as<float>(), dk.as<uint16_t>(), dv.as<uint16_t>(),
-                                       dpos.as<int>(), nh, nkv, hd, max_seq, nullptr);
+            cllm::launch_rope_kv_fused(q, st.dev<float>(si), kc, vc, dpos, nh, nkv, hd, max_seq, nullptr);
         } else {
-            cllm::launch_rope_inplace(dq.as<float>(), dinv.as<float>(), dpos.as<int>(), nh, nkv, hd, nullptr);
-            cllm::launch_kv_write(dq.as<float>(), dk.as<uint16_t>(), dv.as<uint16_t>(), dpos.as<int>(), nh, nkv, hd,
-                                  max_seq, nullptr);
+            cllm::launch_rope_inplace(q, st.dev<float>(si), dpos, nh, nkv, hd, nullptr);
+            cllm::launch_kv_write(q, kc, vc, dpos, nh, nkv, hd, max_seq, nullptr);
         }
-        finish();
-        dq.get(qkv);
-        dk.get(k_cache);
-        dv.get(v_cache);
+        st.finish();
     });
 }
 
 int cudallm_kernel_attention(int impl, const float* q, const unsigned short* k_cache, const unsigned short* v_cache,
                              int ctx, float* out, int nh, int nkv, int hd, int max_seq) {
-    return guarded([&] {
-        CLLM_REQUIRE(q && k_cache && v_cache && out, "cudallm_kernel_attention: null argument");
-        CLLM_REQUIRE(impl == 0 || impl == 1, "cudallm_kernel_attention: impl must be 0 or 1");
-        CLLM_REQUIRE(nh > 0 && nkv > 0 && hd > 0 && max_seq > 0 && ctx >= 1 && ctx <= max_seq,
-                     "cudallm_kernel_attention: bad dimensions");
-        const size_t q_bytes = sizeof(float) * nh * hd;
-        const size_t cache_bytes = sizeof(uint16_t) * static_cast<size_t>(nkv) * max_seq * hd;
+    return abi_entry("cudallm_kernel_attention", [&] {
+        need(impl == 0 || impl == 1, "impl must be 0 (naive) or 1 (split-K)");
+        need(q && k_cache && v_cache && out, "q, both caches and out are required");
+        need(nh > 0 && nkv > 0 && hd > 0 && max_seq > 0, "head counts, head_dim and max_seq must be positive");
+        need(ctx >= 1 && ctx <= max_seq, "ctx must lie in [1, max_seq]");
+        const size_t cache = sizeof(uint16_t) * static_cast<size_t>(nkv) * max_seq * hd;
+        const size_t splits = (static_cast<size_t>(max_seq) + cllm::kAttnChunk - 1) / cllm::kAttnChunk;
         const int pos = ctx - 1;
-        const size_t n_split = (max_seq + cllm::kAttnChunk - 1) / cllm::kAttnChunk;
-        DevBuf dq(q_bytes), dk(cache_bytes), dv(cache_bytes), dpos(sizeof(int)), dout(q_bytes),
-            dpo(impl == 1 ? sizeof(float) * nh * n_split * hd : 0), dpml(impl == 1 ? sizeof(float) * nh * n_split * 2 : 0);
-        dq.put(q);
-        dk.put(k_cache);
-        dv.put(v_cache);
-        dpos.put(&pos);
+        HookStaging st;
+        const int sq = st.add(q, sizeof(float) * nh * hd, HookStaging::In);
+        const int sk = st.add(k_cache, cache, HookStaging::In), sv = st.add(v_cache, cache, HookStaging::In);
+        const int sp = st.add(&pos, sizeof(int), HookStaging::In);
+        const int so = st.add(out, sizeof(float) * nh * hd, HookStaging::Out);
+        const int spo = st.add(nullptr, impl ? sizeof(float) * nh * splits * hd : 0, HookStaging::Scratch);
+        const int spm = st.add(nullptr, impl ? sizeof(float) * nh * splits * 2 : 0, HookStaging::Scratch);
+        st.upload();
         if (impl == 0)
-            cllm::launch_attention_naive(dq.as<float>(), dk.as<uint16_t>(), dv.as<uint16_t>(), dpos.as<int>(),
-                                         dout.as<float>(), nh, nkv, hd, max_seq, nullptr);
+            cllm::launch_attention_naive(st.dev<float>(sq), st.dev<uint16_t>(sk), st.dev<uint16_t>(sv), st.dev<int>(sp),
+                                         st.dev<float>(so), nh, nkv, hd, max_seq, nullptr);
         else
-            cllm::launch_attention_splitk(dq.as<float>(), dk.as<uint16_t>(), dv.as<uint16_t>(), dpos.as<int>(),
-                                          dpo.as<float>(), dpml.as<float>(), dout.as<float>(), nh, nkv, hd, max_seq,
-                                          nullptr);
-        finish();
-        dout.get(out);
+            cllm::launch_attention_splitk(st.dev<float>(sq), st.dev<uint16_t>(sk), st.dev<uint16_t>(sv), st.dev<int>(sp),
+                                          st.dev<float>(spo), st.dev<float>(spm), st.dev<float>(so), nh, nkv, hd,
+                                          max_seq, nullptr);
+        st.finish();
     });
 }
 
 int cudallm_kernel_silu_mul(const float* gu, float* act, int inter) {
-    return guarded([&] {
-        CLLM_REQUIRE(gu && act && inter > 0, "cudallm_kernel_silu_mul: bad argument");
-        DevBuf dgu(sizeof(float) * 2 * inter), dact(sizeof(float) * inter);
-        dgu.put(gu);
-        cllm::launch_silu_mul(dgu.as<float>(), dact.as<float>(), inter, nullptr);
-        finish();
-        dact.get(act);
+    return abi_entry("cudallm_kernel_silu_mul", [&] {
+        need(gu && act && inter > 0, "gu and act are required and inter must be positive");
+        HookStaging st;
+        const int sg = st.add(gu, sizeof(float) * 2 * inter, HookStaging::In);
+        const int sa = st.add(act, sizeof(float) * inter, HookStaging::Out);
+        st.upload();
+        cllm::launch_silu_mul(st.dev<float>(sg), st.dev<float>(sa), inter, nullptr);
+        st.finish();
     });
 }
 
 int cudallm_kernel_argmax(const float* logits, int n, int* out_idx) {
-    return guarded([&] {
-        CLLM_REQUIRE(logits && out_idx && n > 0, "cudallm_kernel_argmax: bad argument");
-        DevBuf dl(sizeof(float) * n), dpv(sizeof(float) * cllm::kArgmaxParts), dpi(sizeof(int) * cllm::kArgmaxParts),
-            dtok(sizeof(int)), dpos(sizeof(int));
-        const int zero = 0;
-        dl.put(logits);
-        dtok.put(&zero);
-        dpos.put(&zero);
-        cllm::launch_argmax(dl.as<float>(), n, dpv.as<float>(), dpi.as<int>(), dtok.as<int>(), dpos.as<int>(), nullptr);
-        finish();
-        dtok.get(out_idx);
+    return abi_entry("cudallm_kernel_argmax", [&] {
+        need(logits && out_idx && n > 0, "logits and out_idx are required and n must be positive");
+        const int zero[2] = {0, 0};  // token and position the kernel writes and advances
+        HookStaging st;
+        const int sl = st.add(logits, sizeof(float) * n, HookStaging::In);
+        const int sv = st.add(nullptr, sizeof(float) * cllm::kArgmaxParts, HookStaging::Scratch);
+        const int si = st.add(nullptr, sizeof(int) * cllm::kArgmaxParts, HookStaging::Scratch);
+        const int stp = st.add(zero, sizeof(zero), HookStaging::In);
+        st.upload();
+        int* tp = st.dev<int>(stp);
+        cllm::launch_argmax(st.dev<float>(sl), n, st.dev<float>(sv), st.dev<int>(si), tp, tp + 1, nullptr);
+        st.finish();
+        CLLM_HIP(hipMemcpy(out_idx, tp, sizeof(int), hipMemcpyDeviceToHost));
     });
 }
 
 int cudallm_launch_matvec(int weight_dtype, int epilogue, int rpb, const void* w, const void* scales, const float* x,
                           const float* norm_w, float eps, float* y, int rows, int cols, void* stream) {
-    return guarded([&] {
-        CLLM_REQUIRE(epilogue >= 0 && epilogue <= 2, "cudallm_launch_matvec: bad epilogue");
-        CLLM_REQUIRE(rpb == 0 || rpb == 1 || rpb == 2 || rpb == 4 || rpb == 8, "cudallm_launch_matvec: bad rpb");
+    return abi_entry("cudallm_launch_matvec", [&] {
         const cllm::WType wt = weight_type(weight_dtype);
-        if (wt == cllm::WType::INT4) CLLM_REQUIRE(cols % 128 == 0, "cudallm_launch_matvec: int4 needs cols % 128 == 0");
-        cllm::MatvecArgs a{w, scales, x, norm_w, eps, y, rows, cols};
+        need(epilogue == 0 || epilogue == 1 || epilogue == 2, "epilogue must be 0, 1 or 2");
+        need(rpb == 0 || rpb == 1 || rpb == 2 || rpb == 4 || rpb == 8, "rpb must be 0, 1, 2, 4 or 8");
+        need(wt != cllm::WType::INT4 || cols % 128 == 0, "int4 weights need cols to be a multiple of 128");
+        const cllm::MatvecArgs a{w, scales, x, norm_w, eps, y, rows, cols};
         cllm::launch_matvec(wt, static_cast<cllm::Epilogue>(epilogue), a, rpb ? rpb : cllm::default_rpb(wt),
                             static_cast<hipStream_t>(stream));
     });
@@ -368,50 +382,61 @@ int cudallm_launch_matvec(int weight_dtype, int epilogue, int rpb, const void* w
 int cudallm_launch_attention(const float* q, const unsigned short* k_cache, const unsigned short* v_cache,
                              const int* d_pos, float* part_o, float* part_ml, float* out, int nh, int nkv, int hd,
                              int max_seq, void* stream) {
-    return guarded([&] {
+    return abi_entry("cudallm_launch_attention", [&] {
         cllm::launch_attention_splitk(q, k_cache, v_cache, d_pos, part_o, part_ml, out, nh, nkv, hd, max_seq,
                                       static_cast<hipStream_t>(stream));
     });
 }
 
+int cudallm_measure_read_bandwidth(unsigned long long bytes, int reps, double* best_gbps, double* median_gbps) {
+    return abi_entry("cudallm_measure_read_bandwidth", [&] {
+        need(best_gbps && median_gbps, "best_gbps and median_gbps are required");
+        const cllm::ReadBandwidth r = cllm::measure_read_bandwidth(bytes, reps);
+        *best_gbps = r.best_gbps;
+        *median_gbps = r.median_gbps;
+    });
+}
+
 int cudallm_quantize_int8_rows(const float* w, int rows, int cols, signed char* q_out, float* scales_out) {
-    return guarded([&] {
-        CLLM_REQUIRE(w && q_out && scales_out && rows > 0 && cols > 0, "cudallm_quantize_int8_rows: bad argument");
+    return abi_entry("cudallm_quantize_int8_rows", [&] {
+        need(w && q_out && scales_out && rows > 0 && cols > 0, "w, q_out and scales_out are required; shape positive");
         const size_t n = static_cast<size_t>(rows) * cols;
-        DevBuf dw(4 * n), dq(n), ds(4ull * rows);
-        dw.put(w);
-        cllm::launch_quantize_int8_rows(dw.as<float>(), rows, cols, dq.as<int8_t>(), ds.as<float>(), nullptr);
-        finish();
-        dq.get(q_out);
-        ds.get(scales_out);
+        HookStaging st;
+        const int sw = st.add(w, 4 * n, HookStaging::In);
+        const int sq = st.add(q_out, n, HookStaging::Out), ss = st.add(scales_out, 4ull * rows, HookStaging::Out);
+        st.upload();
+        cllm::launch_quantize_int8_rows(st.dev<float>(sw), rows, cols, st.dev<int8_t>(sq), st.dev<float>(ss), nullptr);
+        st.finish();
     });
 }
 
 int cudallm_quantize_int4_groups(const float* w, int rows, int cols, int group, unsigned char* packed_out,
                                  unsigned short* scales_out) {
-    return guarded([&] {
-        CLLM_REQUIRE(w && packed_out && scales_out && rows > 0 && cols > 0, "cudallm_quantize_int4_groups: bad argument");
-        CLLM_REQUIRE(group == 128, "cudallm_quantize_int4_groups: group must be 128");
-        CLLM_REQUIRE(cols % 128 == 0, "cudallm_quantize_int4_groups: cols must be a multiple of 128");
+    return abi_entry("cudallm_quantize_int4_groups", [&] {
+        need(w && packed_out && scales_out && rows > 0 && cols > 0, "w, packed_out and scales_out are required; shape positive");
+        need(group == 128, "group must be 128");
+        need(cols % 128 == 0, "cols must be a multiple of 128");
         const size_t n = static_cast<size_t>(rows) * cols;
-        DevBuf dw(4 * n), dp(n / 2), ds(2 * static_cast<size_t>(rows) * (cols / 128));
-        dw.put(w);
-        cllm::launch_quantize_int4_groups(dw.as<float>(), rows, cols, dp.as<uint8_t>(), ds.as<uint16_t>(), nullptr);
-        finish();
-        dp.get(packed_out);
-        ds.get(scales_out);
+        HookStaging st;
+        const int sw = st.add(w, 4 * n, HookStaging::In);
+        const int sp = st.add(packed_out, n / 2, HookStaging::Out);
+        const int ss = st.add(scales_out, 2 * static_cast<size_t>(rows) * (cols / 128), HookStaging::Out);
+        st.upload();
+        cllm::launch_quantize_int4_groups(st.dev<float>(sw), rows, cols, st.dev<uint8_t>(sp), st.dev<uint16_t>(ss),
+                                          nullptr);
+        st.finish();
     });
 }
 
 int cudallm_unpack_int4(const unsigned char* packed, int rows, int cols, signed char* q_out) {
-    return guarded([&] {
-        CLLM_REQUIRE(packed && q_out && rows > 0 && cols > 0 && cols % 2 == 0, "cudallm_unpack_int4: bad argument");
+    return abi_entry("cudallm_unpack_int4", [&] {
+        need(packed && q_out && rows > 0 && cols > 0 && cols % 2 == 0, "packed and q_out are required; cols even and positive");
         const size_t n = static_cast<size_t>(rows) * cols;
-        DevBuf dp(n / 2), dq(n);
-        dp.put(packed);
-        cllm::launch_unpack_int4(dp.as<uint8_t>(), rows, cols, dq.as<int8_t>(), nullptr);
-        finish();
-        dq.get(q_out);
+        HookStaging st;
+        const int sp = st.add(packed, n / 2, HookStaging::In), sq = st.add(q_out, n, HookStaging::Out);
+        st.upload();
+        cllm::launch_unpack_int4(st.dev<uint8_t>(sp), rows, cols, st.dev<int8_t>(sq), nullptr);
+        st.finish();
     });
 }
 

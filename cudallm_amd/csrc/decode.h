@@ -80,9 +80,15 @@ constexpr int kStampSlots = 128;
 constexpr int kDecodeThreads = 512;  // 4 compute waves + 4 loader waves
 // Grid bounds of the decode kernel: each compute wave keeps the residual inputs of its wo/down rows in
 // LDS for at most 8 rows (2048 rows over >= 64 x 4 waves).
+// The loader's row walk needs NW = 4 * grid to be a multiple of 32 (grid % 8 == 0).
 constexpr int kDecodeMinGrid = 64, kDecodeMaxGrid = 4096;
+// Longest context of the decode kernel (Llama-3.2's 131072 positions): 1024 attention splits.
+constexpr int kDecodeMaxSeq = 131072;
+// Tags are (step + 1) * 256 + layer * 8 + phase in 32 bits, so the step counter must stay below 2^24 - 1.  The
+// host clears every tagged buffer and restarts the counter before it gets there.
+constexpr unsigned kDecodeStepLimit = (1u << 24) - 2;
 
-// Enqueue one decode step (one launch).  `grid` workgroups must all be co-resident.
+// Enqueue one decode step (one cooperative launch: every workgroup is co-resident or the launch fails).
 void launch_decode(WType wt, const DecodeParams& p, int grid, hipStream_t s);
 // Workgroups of the decode kernel that fit on the device at once for this weight type.
 int decode_max_grid(WType wt);

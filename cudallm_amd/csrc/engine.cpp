@@ -1,118 +1,191 @@
-// Decode engine.  Op order and step semantics follow reference src/engine/engine.cpp:117-237:
+// Decode engine.  What a step computes is the op order of reference src/engine/engine.cpp:181-237; how
+// it is run is this file's own:
 //
-//   fused:   embedding; per layer { qkv (+attn_norm) ; rope_kv ; attention ; wo (+=x) ;
-//                                   gate_up (+ffn_norm, SwiGLU) ; down (+=x) } ; lm_head (+final_norm) ; argmax
-//   unfused: the same with standalone rmsnorm / add / silu_mul kernels and rope_inplace + kv_write.
+//  * Default options: the persistent decode kernel, one cooperative launch per token.  Its
+//    cross-workgroup handoffs are tagged words (decode.h) whose epochs the host restarts before the
+//    32-bit tags could repeat.
+//  * Ablation options: a step program, the list of kernel launches of one step in op order, built
+//    once at construction.  With cuda_graph the program is captured into a hipGraph on first use and
+//    replayed; step_debug runs it directly with its debug-only entries, device copies of the residual
+//    stream into a snapshot buffer that the host reads once at the end.
 //
-// The token and position live in device memory (argmax writes the token and advances the
-// position), so every step is the same launch: the persistent kernel, or one captured hipGraph of the
-// multi-kernel step; the host only enqueues it.
+// The token and position live in device memory (argmax writes the token and advances the position),
+// so consecutive steps need no host round trip.
 #include "engine.h"
 
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <exception>
 #include <vector>
 
 namespace cllm {
 
 void validate_options(const EngineOptions& o, const ModelConfig& c) {
-    CLLM_REQUIRE(o.matvec == 0 || o.matvec == 1, "matvec_impl must be 0 or 1");
-    CLLM_REQUIRE(o.attn == 0 || o.attn == 1, "attn_impl must be 0 or 1");
-    if (o.matvec == 0) {
-        CLLM_REQUIRE(c.wt == WType::BF16, "the naive matvec needs bf16 weights");
-        CLLM_REQUIRE(!o.fuse, "the naive matvec needs fuse = 0");
-    }
-    CLLM_REQUIRE(o.matvec_rpb == 0 || o.matvec_rpb == 1 || o.matvec_rpb == 2 || o.matvec_rpb == 4 || o.matvec_rpb == 8,
-                 "matvec_rpb must be 0, 1, 2, 4 or 8");
-    CLLM_REQUIRE(o.max_seq_len >= 0 && o.max_seq_len % 128 == 0, "max_seq_len must be 0 or a positive multiple of 128");
-    CLLM_REQUIRE(o.max_seq_len <= c.max_seq_len, "max_seq_len exceeds the file's max_seq_len");
+    const int r = o.matvec_rpb;
+    const struct {
+        bool ok;
+        const char* why;
+    } rules[] = {
+        {o.matvec == 0 || o.matvec == 1, "options: matvec_impl is neither 0 (naive) nor 1 (opt)"},
+        {o.attn == 0 || o.attn == 1, "options: attn_impl is neither 0 (naive) nor 1 (split-K)"},
+        {o.matvec == 1 || c.wt == WType::BF16, "options: the naive matvec only reads bf16 weights"},
+        {o.matvec == 1 || !o.fuse, "options: the naive matvec has no fused epilogues, so it needs fuse = 0"},
+        {r == 0 || r == 1 || r == 2 || r == 4 || r == 8, "options: matvec_rpb takes 0, 1, 2, 4 or 8"},
+        {o.max_seq_len >= 0 && o.max_seq_len % 128 == 0, "options: max_seq_len is neither 0 nor a positive multiple of 128"},
+        {o.max_seq_len <= c.max_seq_len, "options: max_seq_len exceeds the context the file was written for"},
+    };
+    for (const auto& rule : rules)
+        if (!rule.ok) throw ArgError(rule.why);
+}
+
+TraceLayout TraceLayout::of(const ModelConfig& c) {
+    const size_t L = c.n_layers, H = c.hidden, QKV = static_cast<size_t>(c.n_heads + 2 * c.n_kv_heads) * c.head_dim;
+    TraceLayout t{};
+    t.residuals = 0;
+    t.qkv = (L + 1) * H;
+    t.att = t.qkv + L * QKV;
+    t.xa = t.att + L * static_cast<size_t>(c.n_heads) * c.head_dim;
+    t.act = t.xa + L * H;
+    t.total = t.act + L * static_cast<size_t>(c.inter);
+    return t;
 }
 
 namespace {
 
-// Bump allocation inside one arena, 256-byte aligned slots.
-struct Carver {
-    size_t off = 0;
+// Sub-allocations of one arena, each 256-byte aligned.
+class ArenaPlan {
+public:
     template <typename T>
-    size_t take(size_t count) {
-        const size_t at = off;
-        off = (off + count * sizeof(T) + 255) & ~size_t(255);
+    size_t reserve(size_t count) {
+        const size_t at = size_;
+        size_ = (size_ + count * sizeof(T) + 255) / 256 * 256;
         return at;
     }
+    size_t size() const { return size_; }
+
+private:
+    size_t size_ = 0;
 };
+
+// Records everything `record` enqueues on `s` into an executable graph.  The capture is ended on every
+// path, so a failure inside `record` never leaves the stream capturing.
+void capture_graph(hipStream_t s, const std::function<void()>& record, hipGraph_t* graph, hipGraphExec_t* exec) {
+    CLLM_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    std::exception_ptr failed;
+    try {
+        record();
+    } catch (...) {
+        failed = std::current_exception();
+    }
+    hipGraph_t g = nullptr;
+    const hipError_t ended = hipStreamEndCapture(s, &g);
+    if (failed || ended != hipSuccess) {
+        if (g) (void)hipGraphDestroy(g);
+        if (failed) std::rethrow_exception(failed);
+        CLLM_HIP(ended);
+    }
+    const hipError_t made = hipGraphInstantiate(exec, g, nullptr, nullptr, 0);
+    if (made != hipSuccess) {
+        (void)hipGraphDestroy(g);
+        CLLM_HIP(made);
+    }
+    *graph = g;
+}
+
+unsigned env_step_limit() {
+    // Test hook: a smaller epoch limit makes the tag restart happen within a short sequence.
+    const char* v = std::getenv("CUDALLM_EPOCH_LIMIT");
+    if (!v) return kDecodeStepLimit;
+    const unsigned long n = std::strtoul(v, nullptr, 0);
+    return n >= 1 && n < kDecodeStepLimit ? static_cast<unsigned>(n) : kDecodeStepLimit;
+}
 
 }  // namespace
 
 Engine::Engine(const std::string& path, const EngineOptions& opts) : opts_(opts) {
-    {
-        // Validate file and options before any device work.
-        const ParsedFile pf = parse_file(path);
-        validate_options(opts_, pf.config);
-    }
+    // The file and the options are checked before any device work.
+    validate_options(opts_, parse_file(path).config);
     weights_ = std::make_unique<Weights>(path);
     const ModelConfig& c = weights_->config();
     max_seq_ = opts_.max_seq_len ? opts_.max_seq_len : c.max_seq_len;
     rpb_ = opts_.matvec_rpb ? opts_.matvec_rpb : default_rpb(c.wt);
+    step_limit_ = env_step_limit();
     try {
         CLLM_HIP(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
         const size_t H = c.hidden, I = c.inter, V = c.vocab, S = max_seq_, KV = c.n_kv_heads, D = c.head_dim,
-                     NH = c.n_heads, L = c.n_layers, NS = S / kAttnChunk;
-        Carver cv;
-        const size_t o_x = cv.take<float>(H), o_xb = cv.take<float>(H), o_qkv = cv.take<float>((NH + 2 * KV) * D),
-                     o_att = cv.take<float>(NH * D), o_tmp = cv.take<float>(H), o_gu = cv.take<float>(2 * I),
-                     o_act = cv.take<float>(I), o_log = cv.take<float>(V), o_po = cv.take<float>(NH * NS * D),
-                     o_pml = cv.take<float>(NH * NS * 2), o_av = cv.take<float>(kArgmaxParts),
-                     o_ai = cv.take<int>(kArgmaxParts), o_tok = cv.take<int>(1), o_pos = cv.take<int>(1),
-                     o_k = cv.take<uint16_t>(L * KV * S * D), o_v = cv.take<uint16_t>(L * KV * S * D);
-        // Persistent decode kernel: fused + opt options, contexts up to 8192 (one split per lane
-        // in the LSE merge), and one co-resident workgroup per CU (64 to 4096 CUs).  CUDALLM_PERSISTENT=0 selects
-        // the kernel-per-op graph instead (for comparisons).
+                     NH = c.n_heads, L = c.n_layers, NS = S / kAttnChunk, QKV = (NH + 2 * KV) * D;
+
+        // The persistent kernel needs: the default options, a cooperative launch of one workgroup per CU
+        // with the grid a multiple of 8, and a context it supports.  CUDALLM_PERSISTENT=0 selects the
+        // multi-kernel step instead (for comparisons).
+        int dev = 0, coop = 0;
+        CLLM_HIP(hipGetDevice(&dev));
+        CLLM_HIP(hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev));
         const char* env = std::getenv("CUDALLM_PERSISTENT");
-        const bool want = opts_.fuse && opts_.matvec == 1 && opts_.attn == 1 && S <= 8192 && !(env && !std::strcmp(env, "0"));
+        const bool wanted = opts_.fuse && opts_.matvec == 1 && opts_.attn == 1 && !(env && !std::strcmp(env, "0"));
         grid_ = device_cu_count();
-        persistent_ = want && grid_ >= kDecodeMinGrid && grid_ <= kDecodeMaxGrid && decode_max_grid(c.wt) >= grid_;
-        const size_t QKV = (NH + 2 * KV) * D;
-        const size_t o_tx = cv.take<uint64_t>((L + 1) * H), o_txa = cv.take<uint64_t>(L * H),
-                     o_tqkv = cv.take<uint64_t>(L * QKV), o_tatt = cv.take<uint64_t>(L * NH * D),
-                     o_tpart = cv.take<uint64_t>(persistent_ ? L * NH * NS * (D + 2) : 1),
-                     o_tact = cv.take<uint64_t>(L * I), o_targ = cv.take<uint64_t>(2 * 4096),
-                     o_res = cv.take<float>((L + 1) * H), o_layers = cv.take<DecodeLayer>(L),
-                     o_step = cv.take<unsigned>(1), o_err = cv.take<unsigned>(1),
-                     o_stamps = cv.take<unsigned long long>(static_cast<size_t>(grid_) * kStampSlots);
-        CLLM_HIP(hipMalloc(&arena_, cv.off));
-        CLLM_HIP(hipMemset(arena_, 0, cv.off));
-        char* b = static_cast<char*>(arena_);
-        x_ = reinterpret_cast<float*>(b + o_x);
-        xb_ = reinterpret_cast<float*>(b + o_xb);
-        qkv_ = reinterpret_cast<float*>(b + o_qkv);
-        att_ = reinterpret_cast<float*>(b + o_att);
-        tmp_ = reinterpret_cast<float*>(b + o_tmp);
-        gu_ = reinterpret_cast<float*>(b + o_gu);
-        act_ = reinterpret_cast<float*>(b + o_act);
-        logits_ = reinterpret_cast<float*>(b + o_log);
-        part_o_ = reinterpret_cast<float*>(b + o_po);
-        part_ml_ = reinterpret_cast<float*>(b + o_pml);
-        arg_v_ = reinterpret_cast<float*>(b + o_av);
-        arg_i_ = reinterpret_cast<int*>(b + o_ai);
-        d_token_ = reinterpret_cast<int*>(b + o_tok);
-        d_pos_ = reinterpret_cast<int*>(b + o_pos);
-        k_cache_ = reinterpret_cast<uint16_t*>(b + o_k);
-        v_cache_ = reinterpret_cast<uint16_t*>(b + o_v);
-        d_res_ = reinterpret_cast<float*>(b + o_res);
-        d_err_ = reinterpret_cast<unsigned*>(b + o_err);
-        d_stamps_ = reinterpret_cast<unsigned long long*>(b + o_stamps);
+        persistent_ = wanted && coop && S <= static_cast<size_t>(kDecodeMaxSeq) && grid_ % 8 == 0 &&
+                      grid_ >= kDecodeMinGrid && grid_ <= kDecodeMaxGrid && decode_max_grid(c.wt) >= grid_;
+
+        ArenaPlan ap;
+        const size_t at_x = ap.reserve<float>(H), at_xb = ap.reserve<float>(H), at_qkv = ap.reserve<float>(QKV),
+                     at_att = ap.reserve<float>(NH * D), at_tmp = ap.reserve<float>(H), at_gu = ap.reserve<float>(2 * I),
+                     at_act = ap.reserve<float>(I), at_logits = ap.reserve<float>(V),
+                     at_po = ap.reserve<float>(NH * NS * D), at_pml = ap.reserve<float>(NH * NS * 2),
+                     at_av = ap.reserve<float>(kArgmaxParts), at_ai = ap.reserve<int>(kArgmaxParts),
+                     at_tok = ap.reserve<int>(1), at_pos = ap.reserve<int>(1),
+                     at_k = ap.reserve<uint16_t>(L * KV * S * D), at_v = ap.reserve<uint16_t>(L * KV * S * D),
+                     at_res = ap.reserve<float>((L + 1) * H);
+        // Tagged buffers of the persistent kernel, contiguous so that one clear covers them all.
+        const size_t n_part = persistent_ ? L * NH * NS * (D + 2) : 1;
+        const size_t at_tx = ap.reserve<uint64_t>((L + 1) * H), at_txa = ap.reserve<uint64_t>(L * H),
+                     at_tqkv = ap.reserve<uint64_t>(L * QKV), at_tatt = ap.reserve<uint64_t>(L * NH * D),
+                     at_tpart = ap.reserve<uint64_t>(n_part), at_tact = ap.reserve<uint64_t>(L * I),
+                     at_targ = ap.reserve<uint64_t>(2 * kDecodeMaxGrid);
+        const size_t at_tags_end = ap.size();
+        const size_t at_layers = ap.reserve<DecodeLayer>(L), at_step = ap.reserve<unsigned>(1),
+                     at_err = ap.reserve<unsigned>(1),
+                     at_stamps = ap.reserve<unsigned long long>(static_cast<size_t>(grid_) * kStampSlots);
+        CLLM_HIP(hipMalloc(&arena_, ap.size()));
+        CLLM_HIP(hipMemset(arena_, 0, ap.size()));
+        char* base = static_cast<char*>(arena_);
+        auto at = [base](size_t off) { return static_cast<void*>(base + off); };
+        x_ = static_cast<float*>(at(at_x));
+        xb_ = static_cast<float*>(at(at_xb));
+        qkv_ = static_cast<float*>(at(at_qkv));
+        att_ = static_cast<float*>(at(at_att));
+        tmp_ = static_cast<float*>(at(at_tmp));
+        gu_ = static_cast<float*>(at(at_gu));
+        act_ = static_cast<float*>(at(at_act));
+        logits_ = static_cast<float*>(at(at_logits));
+        part_o_ = static_cast<float*>(at(at_po));
+        part_ml_ = static_cast<float*>(at(at_pml));
+        arg_v_ = static_cast<float*>(at(at_av));
+        arg_i_ = static_cast<int*>(at(at_ai));
+        d_token_ = static_cast<int*>(at(at_tok));
+        d_pos_ = static_cast<int*>(at(at_pos));
+        k_cache_ = static_cast<uint16_t*>(at(at_k));
+        v_cache_ = static_cast<uint16_t*>(at(at_v));
+        d_res_ = static_cast<float*>(at(at_res));
+        tags_begin_ = at(at_tx);
+        tags_bytes_ = at_tags_end - at_tx;
+        d_stamps_ = static_cast<unsigned long long*>(at(at_stamps));
+
         const Weights& W = *weights_;
-        std::vector<DecodeLayer> table(L);
-        for (size_t l = 0; l < L; ++l) {
-            const LayerWeights& lw = W.layers[l];
-            table[l] = {lw.attn_norm, lw.wqkv.w, lw.wqkv.scales, lw.wo.w, lw.wo.scales,
-                        lw.ffn_norm, lw.w_gate_up.w, lw.w_gate_up.scales, lw.w_down.w, lw.w_down.scales};
-        }
-        auto* d_layers = reinterpret_cast<DecodeLayer*>(b + o_layers);
+        std::vector<DecodeLayer> table;
+        table.reserve(L);
+        for (const LayerWeights& lw : W.layers)
+            table.push_back({lw.attn_norm, lw.wqkv.w, lw.wqkv.scales, lw.wo.w, lw.wo.scales, lw.ffn_norm,
+                             lw.w_gate_up.w, lw.w_gate_up.scales, lw.w_down.w, lw.w_down.scales});
+        auto* d_layers = static_cast<DecodeLayer*>(at(at_layers));
         CLLM_HIP(hipMemcpy(d_layers, table.data(), sizeof(DecodeLayer) * L, hipMemcpyHostToDevice));
-        const unsigned one = 1;  // tags of step 0 would equal the zero-filled buffers
-        CLLM_HIP(hipMemcpy(b + o_step, &one, sizeof(one), hipMemcpyHostToDevice));
+        // The first launch uses step 1: tags of step 0 could only be confused with never-written words if the
+        // counter started at -1, but starting at 1 keeps every live tag away from the zero-filled arena.
+        const unsigned first_step = 1;
+        CLLM_HIP(hipMemcpy(at(at_step), &first_step, sizeof(first_step), hipMemcpyHostToDevice));
+
+        dp_ = DecodeParams{};
         dp_.layers = d_layers;
         dp_.emb = W.tok_embeddings.w;
         dp_.emb_s = W.tok_embeddings.scales;
@@ -121,23 +194,23 @@ Engine::Engine(const std::string& path, const EngineOptions& opts) : opts_(opts)
         dp_.k_cache = k_cache_;
         dp_.v_cache = v_cache_;
         dp_.max_seq = max_seq_;
-        dp_.tx = reinterpret_cast<uint64_t*>(b + o_tx);
-        dp_.txa = reinterpret_cast<uint64_t*>(b + o_txa);
-        dp_.tqkv = reinterpret_cast<uint64_t*>(b + o_tqkv);
-        dp_.tatt = reinterpret_cast<uint64_t*>(b + o_tatt);
-        dp_.tpart = reinterpret_cast<uint64_t*>(b + o_tpart);
-        dp_.tact = reinterpret_cast<uint64_t*>(b + o_tact);
-        dp_.targ = reinterpret_cast<uint64_t*>(b + o_targ);
+        dp_.tx = static_cast<uint64_t*>(at(at_tx));
+        dp_.txa = static_cast<uint64_t*>(at(at_txa));
+        dp_.tqkv = static_cast<uint64_t*>(at(at_tqkv));
+        dp_.tatt = static_cast<uint64_t*>(at(at_tatt));
+        dp_.tpart = static_cast<uint64_t*>(at(at_tpart));
+        dp_.tact = static_cast<uint64_t*>(at(at_tact));
+        dp_.targ = static_cast<uint64_t*>(at(at_targ));
         dp_.logits = logits_;
         dp_.d_token = d_token_;
         dp_.d_pos = d_pos_;
-        dp_.d_step = reinterpret_cast<unsigned*>(b + o_step);
-        dp_.d_err = d_err_;
-        dp_.residuals = nullptr;
-        dp_.stamps = nullptr;
+        dp_.d_step = static_cast<unsigned*>(at(at_step));
+        dp_.d_err = static_cast<unsigned*>(at(at_err));
         dp_.eps = c.rms_eps;
-        const char* stall = std::getenv("CUDALLM_STALL");  // timing perturbation for tests only
+        const char* stall = std::getenv("CUDALLM_STALL");  // timing perturbation, tests only
         dp_.stall = stall ? static_cast<unsigned>(std::strtoul(stall, nullptr, 0)) : 0u;
+
+        if (!persistent_) build_program();
         CLLM_HIP(hipDeviceSynchronize());
     } catch (...) {
         release();
@@ -146,16 +219,16 @@ Engine::Engine(const std::string& path, const EngineOptions& opts) : opts_(opts)
 }
 
 void Engine::release() noexcept {
-    auto report = [](hipError_t e, const char* what) {
-        if (e != hipSuccess) std::fprintf(stderr, "cudallm: %s in ~Engine: %s\n", what, hipGetErrorString(e));
+    auto check = [](hipError_t e, const char* what) {
+        if (e != hipSuccess) std::fprintf(stderr, "cudallm: %s while destroying an engine: %s\n", what, hipGetErrorString(e));
     };
-    if (exec_) report(hipGraphExecDestroy(exec_), "hipGraphExecDestroy");
-    if (graph_) report(hipGraphDestroy(graph_), "hipGraphDestroy");
-    exec_ = nullptr;
+    if (graph_exec_) check(hipGraphExecDestroy(graph_exec_), "hipGraphExecDestroy");
+    if (graph_) check(hipGraphDestroy(graph_), "hipGraphDestroy");
+    graph_exec_ = nullptr;
     graph_ = nullptr;
-    if (arena_) report(hipFree(arena_), "hipFree");
+    if (arena_) check(hipFree(arena_), "hipFree");
     arena_ = nullptr;
-    if (stream_) report(hipStreamDestroy(stream_), "hipStreamDestroy");
+    if (stream_) check(hipStreamDestroy(stream_), "hipStreamDestroy");
     stream_ = nullptr;
 }
 
@@ -164,164 +237,237 @@ Engine::~Engine() {
     release();
 }
 
-void Engine::check_device_error() {
-    unsigned e = 0;
-    CLLM_HIP(hipMemcpy(&e, d_err_, sizeof(e), hipMemcpyDeviceToHost));
-    if (e) {
-        throw DeviceError(
-            "persistent decode kernel: a cross-workgroup wait exceeded its bound (were all workgroups "
-            "co-resident? another process may be sharing the GPU); the results of this sequence are invalid");
-    }
-}
+// ---- the multi-kernel step ------------------------------------------------------------------
 
-void Engine::reset() {
-    CLLM_HIP(hipStreamSynchronize(stream_));
-    if (persistent_) check_device_error();
-    launch_set_token(d_pos_, 0, stream_);  // a kernel, not a memset
-    CLLM_HIP(hipStreamSynchronize(stream_));
-    host_pos_ = 0;
-}
-
-void Engine::step(int token, float* logits_out, int* next_token_out) {
-    if (host_pos_ >= max_seq_) throw SequenceFull("step: the sequence is full (pos == max_seq_len); call reset()");
-    CLLM_REQUIRE(token >= -1 && token < config().vocab, "step: token out of range");
-    if (token >= 0) launch_set_token(d_token_, token, stream_);
-    // The persistent step is one kernel, launched directly with or without cuda_graph: replaying it as a one-node
-    // graph left 8.8 us between consecutive kernels on MI355X against 4.1 us for a plain launch.  The
-    // multi-kernel step is captured once and replayed.
-    if (opts_.graph && !persistent_) {
-        if (!exec_) {
-            CLLM_HIP(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
-            try {
-                enqueue_forward(nullptr);
-            } catch (...) {
-                hipGraph_t broken = nullptr;
-                (void)hipStreamEndCapture(stream_, &broken);
-                if (broken) (void)hipGraphDestroy(broken);
-                throw;
-            }
-            CLLM_HIP(hipStreamEndCapture(stream_, &graph_));
-            CLLM_HIP(hipGraphInstantiate(&exec_, graph_, nullptr, nullptr, 0));
-        }
-        CLLM_HIP(hipGraphLaunch(exec_, stream_));
-    } else if (persistent_) {
-        launch_decode(config().wt, dp_, grid_, stream_);
-    } else {
-        enqueue_forward(nullptr);
-    }
-    host_pos_ += 1;
-    if (logits_out || next_token_out) {
-        CLLM_HIP(hipStreamSynchronize(stream_));
-        if (persistent_) check_device_error();
-        if (logits_out)
-            CLLM_HIP(hipMemcpy(logits_out, logits_, sizeof(float) * config().vocab, hipMemcpyDeviceToHost));
-        if (next_token_out) CLLM_HIP(hipMemcpy(next_token_out, d_token_, sizeof(int), hipMemcpyDeviceToHost));
-    }
-}
-
-void Engine::step_debug(int token, float* residuals_out, float* logits_out, int* next_token_out) {
-    if (host_pos_ >= max_seq_) throw SequenceFull("step_debug: the sequence is full (pos == max_seq_len); call reset()");
-    CLLM_REQUIRE(token >= -1 && token < config().vocab, "step_debug: token out of range");
-    CLLM_REQUIRE(residuals_out, "step_debug: residuals_out is null");
-    if (token >= 0) launch_set_token(d_token_, token, stream_);
-    if (persistent_) {
-        DecodeParams p = dp_;
-        p.residuals = d_res_;
-        launch_decode(config().wt, p, grid_, stream_);
-    } else {
-        enqueue_forward(residuals_out);
-    }
-    host_pos_ += 1;
-    CLLM_HIP(hipStreamSynchronize(stream_));
-    if (persistent_) {
-        check_device_error();
-        const ModelConfig& c = config();
-        CLLM_HIP(hipMemcpy(residuals_out, d_res_, sizeof(float) * (c.n_layers + 1) * c.hidden, hipMemcpyDeviceToHost));
-    }
-    if (logits_out) CLLM_HIP(hipMemcpy(logits_out, logits_, sizeof(float) * config().vocab, hipMemcpyDeviceToHost));
-    if (next_token_out) CLLM_HIP(hipMemcpy(next_token_out, d_token_, sizeof(int), hipMemcpyDeviceToHost));
-}
-
-int Engine::step_profile(int token, unsigned long long* stamps_out, long capacity) {
-    if (!persistent_) throw StateError("step_profile: this engine does not use the persistent decode kernel");
-    if (host_pos_ >= max_seq_) throw SequenceFull("step_profile: the sequence is full (pos == max_seq_len); call reset()");
-    CLLM_REQUIRE(token >= -1 && token < config().vocab, "step_profile: token out of range");
-    CLLM_REQUIRE(stamps_out && capacity >= static_cast<long>(grid_) * kStampSlots,
-                 "step_profile: stamps_out must hold grid * 128 values");
-    if (token >= 0) launch_set_token(d_token_, token, stream_);
-    CLLM_HIP(hipMemsetAsync(d_stamps_, 0, sizeof(unsigned long long) * grid_ * kStampSlots, stream_));
-    DecodeParams p = dp_;
-    p.stamps = d_stamps_;
-    launch_decode(config().wt, p, grid_, stream_);
-    host_pos_ += 1;
-    CLLM_HIP(hipStreamSynchronize(stream_));
-    check_device_error();
-    CLLM_HIP(hipMemcpy(stamps_out, d_stamps_, sizeof(unsigned long long) * grid_ * kStampSlots, hipMemcpyDeviceToHost));
-    return grid_;
-}
-
-void Engine::linear(const Linear& L, const float* x, float* y, Epilogue ep, const float* norm_w) {
-    MatvecArgs a{L.w, L.scales, x, norm_w, config().rms_eps, y, L.rows, L.cols};
-    if (opts_.matvec == 0) {
-        CLLM_INTERNAL(ep == Epilogue::STORE && !norm_w, "naive matvec: STORE only");
-        launch_matvec_naive(a, stream_);
-    } else {
-        launch_matvec(L.wt, ep, a, rpb_, stream_);
-    }
-}
-
-void Engine::enqueue_forward(float* residuals_out) {
+void Engine::build_program() {
     const ModelConfig& c = config();
     const Weights& W = *weights_;
-    const int H = c.hidden, NH = c.n_heads, KV = c.n_kv_heads, D = c.head_dim;
-    const size_t layer_cache = static_cast<size_t>(KV) * max_seq_ * D;
-    auto snapshot = [&](int k) {
-        if (!residuals_out) return;
-        CLLM_HIP(hipStreamSynchronize(stream_));
-        CLLM_HIP(hipMemcpy(residuals_out + static_cast<size_t>(k) * H, x_, sizeof(float) * H, hipMemcpyDeviceToHost));
+    const int H = c.hidden, NH = c.n_heads, KV = c.n_kv_heads, D = c.head_dim, I = c.inter, ms = max_seq_;
+    const float eps = c.rms_eps;
+    const size_t cache_stride = static_cast<size_t>(KV) * max_seq_ * D;
+    const bool naive_mv = opts_.matvec == 0, naive_attn = opts_.attn == 0;
+    const int rpb = rpb_;
+    auto emit = [this](std::function<void(hipStream_t)> f) { program_.push_back({false, std::move(f)}); };
+    auto snapshot = [this, H](int k) {
+        float* dst = d_res_ + static_cast<size_t>(k) * H;
+        const float* src = x_;
+        program_.push_back({true, [dst, src, H](hipStream_t s) {
+                                CLLM_HIP(hipMemcpyAsync(dst, src, sizeof(float) * H, hipMemcpyDeviceToDevice, s));
+                            }});
     };
-    const Linear& E = W.tok_embeddings;
-    launch_embedding(E.wt, E.w, E.scales, d_token_, x_, H, c.vocab, c.group_size, stream_);
+    auto matvec = [&](const Linear& L, const float* in, float* out, Epilogue ep, const float* norm_w) {
+        const MatvecArgs a{L.w, L.scales, in, norm_w, eps, out, L.rows, L.cols};
+        const WType wt = L.wt;
+        if (naive_mv) {
+            CLLM_INTERNAL(ep == Epilogue::STORE && !norm_w, "naive matvec: STORE without a fused norm only");
+            emit([a](hipStream_t s) { launch_matvec_naive(a, s); });
+        } else {
+            emit([a, wt, ep, rpb](hipStream_t s) { launch_matvec(wt, ep, a, rpb, s); });
+        }
+    };
+    float *x = x_, *xb = xb_, *qkv = qkv_, *att = att_, *tmp = tmp_, *gu = gu_, *act = act_;
+    const int* pos = d_pos_;
+    auto attention = [&](const uint16_t* kl, const uint16_t* vl) {
+        if (naive_attn) {
+            emit([=](hipStream_t s) { launch_attention_naive(qkv, kl, vl, pos, att, NH, KV, D, ms, s); });
+        } else {
+            float *po = part_o_, *pml = part_ml_;
+            emit([=](hipStream_t s) { launch_attention_splitk(qkv, kl, vl, pos, po, pml, att, NH, KV, D, ms, s); });
+        }
+    };
+
+    {
+        const Linear E = W.tok_embeddings;
+        const int* tok = d_token_;
+        const int V = c.vocab, g = c.group_size;
+        emit([=](hipStream_t s) { launch_embedding(E.wt, E.w, E.scales, tok, x, H, V, g, s); });
+    }
     snapshot(0);
     for (int l = 0; l < c.n_layers; ++l) {
-        const LayerWeights& L = W.layers[l];
-        uint16_t* kl = k_cache_ + l * layer_cache;
-        uint16_t* vl = v_cache_ + l * layer_cache;
+        const LayerWeights& lw = W.layers[l];
+        uint16_t* kl = k_cache_ + l * cache_stride;
+        uint16_t* vl = v_cache_ + l * cache_stride;
+        const float* inv_freq = W.inv_freq;
         if (opts_.fuse) {
-            linear(L.wqkv, x_, qkv_, Epilogue::STORE, L.attn_norm);
-            launch_rope_kv_fused(qkv_, W.inv_freq, kl, vl, d_pos_, NH, KV, D, max_seq_, stream_);
+            matvec(lw.wqkv, x, qkv, Epilogue::STORE, lw.attn_norm);
+            emit([=](hipStream_t s) { launch_rope_kv_fused(qkv, inv_freq, kl, vl, pos, NH, KV, D, ms, s); });
+            attention(kl, vl);
+            matvec(lw.wo, att, x, Epilogue::ADD, nullptr);
+            matvec(lw.w_gate_up, x, act, Epilogue::SWIGLU, lw.ffn_norm);
+            matvec(lw.w_down, act, x, Epilogue::ADD, nullptr);
         } else {
-            launch_rmsnorm(x_, L.attn_norm, c.rms_eps, xb_, H, stream_);
-            linear(L.wqkv, xb_, qkv_, Epilogue::STORE, nullptr);
-            launch_rope_inplace(qkv_, W.inv_freq, d_pos_, NH, KV, D, stream_);
-            launch_kv_write(qkv_, kl, vl, d_pos_, NH, KV, D, max_seq_, stream_);
-        }
-        if (opts_.attn == 0)
-            launch_attention_naive(qkv_, kl, vl, d_pos_, att_, NH, KV, D, max_seq_, stream_);
-        else
-            launch_attention_splitk(qkv_, kl, vl, d_pos_, part_o_, part_ml_, att_, NH, KV, D, max_seq_, stream_);
-        if (opts_.fuse) {
-            linear(L.wo, att_, x_, Epilogue::ADD, nullptr);
-            linear(L.w_gate_up, x_, act_, Epilogue::SWIGLU, L.ffn_norm);
-            linear(L.w_down, act_, x_, Epilogue::ADD, nullptr);
-        } else {
-            linear(L.wo, att_, tmp_, Epilogue::STORE, nullptr);
-            launch_add_inplace(x_, tmp_, H, stream_);
-            launch_rmsnorm(x_, L.ffn_norm, c.rms_eps, xb_, H, stream_);
-            linear(L.w_gate_up, xb_, gu_, Epilogue::STORE, nullptr);
-            launch_silu_mul(gu_, act_, c.inter, stream_);
-            linear(L.w_down, act_, tmp_, Epilogue::STORE, nullptr);
-            launch_add_inplace(x_, tmp_, H, stream_);
+            const float *an = lw.attn_norm, *fn = lw.ffn_norm;
+            emit([=](hipStream_t s) { launch_rmsnorm(x, an, eps, xb, H, s); });
+            matvec(lw.wqkv, xb, qkv, Epilogue::STORE, nullptr);
+            emit([=](hipStream_t s) { launch_rope_inplace(qkv, inv_freq, pos, NH, KV, D, s); });
+            emit([=](hipStream_t s) { launch_kv_write(qkv, kl, vl, pos, NH, KV, D, ms, s); });
+            attention(kl, vl);
+            matvec(lw.wo, att, tmp, Epilogue::STORE, nullptr);
+            emit([=](hipStream_t s) { launch_add_inplace(x, tmp, H, s); });
+            emit([=](hipStream_t s) { launch_rmsnorm(x, fn, eps, xb, H, s); });
+            matvec(lw.w_gate_up, xb, gu, Epilogue::STORE, nullptr);
+            emit([=](hipStream_t s) { launch_silu_mul(gu, act, I, s); });
+            matvec(lw.w_down, act, tmp, Epilogue::STORE, nullptr);
+            emit([=](hipStream_t s) { launch_add_inplace(x, tmp, H, s); });
         }
         snapshot(l + 1);
     }
     if (opts_.fuse) {
-        linear(E, x_, logits_, Epilogue::STORE, W.final_norm);
+        matvec(W.tok_embeddings, x, logits_, Epilogue::STORE, W.final_norm);
     } else {
-        launch_rmsnorm(x_, W.final_norm, c.rms_eps, xb_, H, stream_);
-        linear(E, xb_, logits_, Epilogue::STORE, nullptr);
+        const float* fn = W.final_norm;
+        emit([=](hipStream_t s) { launch_rmsnorm(x, fn, eps, xb, H, s); });
+        matvec(W.tok_embeddings, xb, logits_, Epilogue::STORE, nullptr);
     }
-    launch_argmax(logits_, c.vocab, arg_v_, arg_i_, d_token_, d_pos_, stream_);
+    float *lg = logits_, *av = arg_v_;
+    int *ai = arg_i_, *tok = d_token_, *dpos = d_pos_;
+    const int V = c.vocab;
+    emit([=](hipStream_t s) { launch_argmax(lg, V, av, ai, tok, dpos, s); });
+}
+
+void Engine::run_program(bool debug) {
+    for (const Op& op : program_)
+        if (debug || !op.debug_only) op.enqueue(stream_);
+}
+
+// ---- the persistent step --------------------------------------------------------------------
+
+void Engine::launch_persistent(const DecodeParams& p) {
+    if (launches_ >= step_limit_) {
+        // Restart the epochs before the 32-bit tags could repeat: with every tagged word zero and the step
+        // counter back at 0, no word written under the old numbering can carry a tag of the new one.
+        CLLM_HIP(hipMemsetAsync(tags_begin_, 0, tags_bytes_, stream_));
+        CLLM_HIP(hipMemsetAsync(dp_.d_step, 0, sizeof(unsigned), stream_));
+        launches_ = 0;
+    }
+    launch_decode(config().wt, p, grid_, stream_);
+    ++launches_;
+}
+
+void Engine::raise_if_kernel_failed() {
+    if (!persistent_) return;
+    unsigned flag = 0;
+    CLLM_HIP(hipMemcpy(&flag, dp_.d_err, sizeof(flag), hipMemcpyDeviceToHost));
+    if (flag)
+        throw DeviceError(
+            "persistent decode kernel: a wait on another workgroup ran past its bound, so this sequence's results are "
+            "invalid; reset() starts a new sequence");
+}
+
+// ---- steps ----------------------------------------------------------------------------------
+
+void Engine::reset() {
+    CLLM_HIP(hipStreamSynchronize(stream_));
+    unsigned flag = 0;
+    if (persistent_) {
+        CLLM_HIP(hipMemcpy(&flag, dp_.d_err, sizeof(flag), hipMemcpyDeviceToHost));
+        if (flag) CLLM_HIP(hipMemsetAsync(dp_.d_err, 0, sizeof(unsigned), stream_));
+    }
+    launch_set_token(d_pos_, 0, stream_);  // position 0 (a kernel, not a memset)
+    CLLM_HIP(hipStreamSynchronize(stream_));
+    host_pos_ = 0;
+    if (flag)
+        throw DeviceError(
+            "persistent decode kernel: the previous sequence had a wait that ran past its bound (its results were "
+            "invalid); the engine is reset and usable");
+}
+
+void Engine::begin_step(const char* who, int token) {
+    if (host_pos_ >= max_seq_)
+        throw SequenceFull(std::string(who) + ": sequence full at max_seq_len positions; reset() starts a new one");
+    if (token < -1 || token >= config().vocab)
+        throw ArgError(std::string(who) + ": token must be -1 or a vocabulary index");
+    if (token >= 0) launch_set_token(d_token_, token, stream_);
+}
+
+void Engine::read_outputs(float* logits_out, int* next_token_out) {
+    if (logits_out) CLLM_HIP(hipMemcpy(logits_out, logits_, sizeof(float) * config().vocab, hipMemcpyDeviceToHost));
+    if (next_token_out) CLLM_HIP(hipMemcpy(next_token_out, d_token_, sizeof(int), hipMemcpyDeviceToHost));
+}
+
+void Engine::step(int token, float* logits_out, int* next_token_out) {
+    begin_step("step", token);
+    // The persistent step is one kernel launched directly whether or not cuda_graph is set (a cooperative
+    // launch; replaying a one-node graph of it only adds launch latency).  The multi-kernel program is captured
+    // on first use and replayed.
+    if (persistent_) {
+        launch_persistent(dp_);
+    } else if (opts_.graph) {
+        if (!graph_exec_) capture_graph(stream_, [this] { run_program(false); }, &graph_, &graph_exec_);
+        CLLM_HIP(hipGraphLaunch(graph_exec_, stream_));
+    } else {
+        run_program(false);
+    }
+    host_pos_ += 1;
+    if (!logits_out && !next_token_out) return;  // fully asynchronous
+    CLLM_HIP(hipStreamSynchronize(stream_));
+    raise_if_kernel_failed();
+    read_outputs(logits_out, next_token_out);
+}
+
+void Engine::step_debug(int token, float* residuals_out, float* logits_out, int* next_token_out) {
+    CLLM_REQUIRE(residuals_out, "step_debug: residuals_out is required");
+    begin_step("step_debug", token);
+    if (persistent_) {
+        DecodeParams p = dp_;
+        p.residuals = d_res_;
+        launch_persistent(p);
+    } else {
+        run_program(true);
+    }
+    host_pos_ += 1;
+    CLLM_HIP(hipStreamSynchronize(stream_));
+    raise_if_kernel_failed();
+    const ModelConfig& c = config();
+    CLLM_HIP(hipMemcpy(residuals_out, d_res_, sizeof(float) * (c.n_layers + 1) * c.hidden, hipMemcpyDeviceToHost));
+    read_outputs(logits_out, next_token_out);
+}
+
+int Engine::step_profile(int token, unsigned long long* stamps_out, long capacity) {
+    if (!persistent_) throw StateError("step_profile: this engine's options do not select the persistent decode kernel");
+    CLLM_REQUIRE(stamps_out && capacity >= static_cast<long>(grid_) * kStampSlots,
+                 "step_profile: stamps_out must hold grid * 128 values");
+    begin_step("step_profile", token);
+    const size_t bytes = sizeof(unsigned long long) * grid_ * kStampSlots;
+    CLLM_HIP(hipMemsetAsync(d_stamps_, 0, bytes, stream_));
+    DecodeParams p = dp_;
+    p.stamps = d_stamps_;
+    launch_persistent(p);
+    host_pos_ += 1;
+    CLLM_HIP(hipStreamSynchronize(stream_));
+    raise_if_kernel_failed();
+    CLLM_HIP(hipMemcpy(stamps_out, d_stamps_, bytes, hipMemcpyDeviceToHost));
+    return grid_;
+}
+
+void Engine::step_trace(int token, float* trace_out, long capacity, float* logits_out, int* next_token_out) {
+    if (!persistent_) throw StateError("step_trace: this engine's options do not select the persistent decode kernel");
+    const ModelConfig& c = config();
+    const TraceLayout t = TraceLayout::of(c);
+    CLLM_REQUIRE(trace_out && capacity >= static_cast<long>(t.total), "step_trace: trace_out is too small");
+    begin_step("step_trace", token);
+    DecodeParams p = dp_;
+    p.residuals = d_res_;
+    launch_persistent(p);
+    host_pos_ += 1;
+    CLLM_HIP(hipStreamSynchronize(stream_));
+    raise_if_kernel_failed();
+    CLLM_HIP(hipMemcpy(trace_out + t.residuals, d_res_, sizeof(float) * (c.n_layers + 1) * c.hidden,
+                       hipMemcpyDeviceToHost));
+    // Each tagged word holds its fp32 value in the low half.
+    auto unpack = [&](const uint64_t* src, size_t n, float* dst) {
+        std::vector<uint64_t> words(n);
+        CLLM_HIP(hipMemcpy(words.data(), src, sizeof(uint64_t) * n, hipMemcpyDeviceToHost));
+        for (size_t i = 0; i < n; ++i) {
+            const uint32_t bits = static_cast<uint32_t>(words[i]);
+            std::memcpy(dst + i, &bits, sizeof(bits));
+        }
+    };
+    unpack(dp_.tqkv, t.att - t.qkv, trace_out + t.qkv);
+    unpack(dp_.tatt, t.xa - t.att, trace_out + t.att);
+    unpack(dp_.txa, t.act - t.xa, trace_out + t.xa);
+    unpack(dp_.tact, t.total - t.act, trace_out + t.act);
+    read_outputs(logits_out, next_token_out);
 }
 
 }  // namespace cllm

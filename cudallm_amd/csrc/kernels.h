@@ -61,4 +61,12 @@ void launch_unpack_int4(const uint8_t* packed, int rows, int cols, int8_t* q, hi
 
 int device_cu_count();
 
+// Stream-read bandwidth of device memory over a `bytes` buffer: best and median GB/s of `reps` timed reads
+// for the best of a few launch shapes (the read peak the roofline fractions are also quoted against).
+struct ReadBandwidth {
+    double best_gbps = 0, median_gbps = 0;
+    int blocks_per_cu = 0, loads_in_flight = 0;
+};
+ReadBandwidth measure_read_bandwidth(size_t bytes, int reps);
+
 }  // namespace cllm

@@ -1283,48 +1283,83 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
         }
         stamp(p, 1 + 6 * l + 1);
 
-        // ---- LSE merge of the splits: one wave per head, lane s holds split s (nsplit <= 64) ----
+        // ---- LSE merge of the splits: one wave per head, lane s holds split s of each 64-split block ----
         renew();
         if (nsplit > 1) {
+            const unsigned tag = tg + T_ATT_PART;
 #pragma unroll 1
             for (int h = gw; h < NH; h += NW) {
                 const uint64_t* pp = tpart + static_cast<size_t>(h) * NS * kPartStride;
-                const unsigned tag = tg + T_ATT_PART;
-                // One round trip for the first 16 splits: each lane's (m, l) and the o values all in flight at once.
-                uint64_t vm = static_cast<uint64_t>(tag) << 32, vl = vm;
-                if (lane < nsplit) {
-                    vm = tload(pp + lane * kPartStride + HD);
-                    vl = tload(pp + lane * kPartStride + HD + 1);
-                }
-                float M = 0.f, e = 0.f, Lsum = 0.f, acc = 0.f;
-#pragma unroll 1
-                for (int sb = 0; sb < nsplit; sb += 16) {
-                    uint64_t v[16];
+                // (m, l) of split sb + lane, polled until tagged; one round trip for the whole block.
+                auto poll_ml = [&](int sb, float& ms, float& ls) {
+                    const bool in = sb + lane < nsplit;
+                    uint64_t vm = static_cast<uint64_t>(tag) << 32, vl = vm;
+                    if (in) {
+                        vm = tload(pp + (sb + lane) * kPartStride + HD);
+                        vl = tload(pp + (sb + lane) * kPartStride + HD + 1);
+                    }
+                    unsigned spins = 0;
+                    while (!(tagged(vm, tag) && tagged(vl, tag)) && !give_up(spins, err)) {
+                        if (!tagged(vm, tag)) vm = tload(pp + (sb + lane) * kPartStride + HD);
+                        if (!tagged(vl, tag)) vl = tload(pp + (sb + lane) * kPartStride + HD + 1);
+                    }
+                    ms = in ? tvalue(vm) : -INFINITY;
+                    ls = in ? tvalue(vl) : 0.f;
+                };
+                // The o values of splits 0..15 are loaded together with block 0's (m, l): one round trip for
+                // contexts up to 2048.
+                auto load_o = [&](int sb, int end, uint64_t (&v)[16]) {
 #pragma unroll
                     for (int k = 0; k < 16; ++k)
-                        v[k] = sb + k < nsplit ? tload(pp + (sb + k) * kPartStride + lane) : static_cast<uint64_t>(tag) << 32;
+                        v[k] = sb + k < end ? tload(pp + (sb + k) * kPartStride + lane) : static_cast<uint64_t>(tag) << 32;
+                };
+                auto poll_o = [&](int sb, int end, uint64_t (&v)[16]) {
                     unsigned spins = 0;
                     for (;;) {
-                        bool ok = tagged(vm, tag) && tagged(vl, tag);
+                        bool ok = true;
 #pragma unroll
                         for (int k = 0; k < 16; ++k) ok = ok && tagged(v[k], tag);
                         if (ok || give_up(spins, err)) break;
-                        if (!tagged(vm, tag)) vm = tload(pp + lane * kPartStride + HD);
-                        if (!tagged(vl, tag)) vl = tload(pp + lane * kPartStride + HD + 1);
 #pragma unroll
                         for (int k = 0; k < 16; ++k)
-                            if (sb + k < nsplit && !tagged(v[k], tag)) v[k] = tload(pp + (sb + k) * kPartStride + lane);
+                            if (sb + k < end && !tagged(v[k], tag)) v[k] = tload(pp + (sb + k) * kPartStride + lane);
                     }
-                    if (sb == 0) {
-                        const float ms = lane < nsplit ? tvalue(vm) : -INFINITY;
-                        const float ls = lane < nsplit ? tvalue(vl) : 0.f;
-                        M = wave_max(ms);
-                        e = lane < nsplit ? expf(ms - M) : 0.f;
-                        Lsum = wave_sum(ls * e);
-                    }
+                };
+                uint64_t v0[16];
+                load_o(0, min(nsplit, kWave), v0);
+                // Pass 1: the maximum over every split (one block of 64 up to context 8192).
+                float ms0, ls0;
+                poll_ml(0, ms0, ls0);
+                float M = wave_max(ms0);
+#pragma unroll 1
+                for (int sb = kWave; sb < nsplit; sb += kWave) {
+                    float ms, ls;
+                    poll_ml(sb, ms, ls);
+                    M = fmaxf(M, wave_max(ms));
+                }
+                // Pass 2: L and the weighted o, splits in order, 16 o values in flight per round trip.
+                float Lsum = 0.f, acc = 0.f;
+#pragma unroll 1
+                for (int sb64 = 0; sb64 < nsplit; sb64 += kWave) {
+                    float ms = ms0, ls = ls0;
+                    if (sb64 > 0) poll_ml(sb64, ms, ls);
+                    const float e = sb64 + lane < nsplit ? expf(ms - M) : 0.f;
+                    Lsum += wave_sum(ls * e);
+                    const int end = min(nsplit, sb64 + kWave);
+#pragma unroll 1
+                    for (int sb = sb64; sb < end; sb += 16) {
+                        uint64_t v[16];
+                        if (sb == 0) {
 #pragma unroll
-                    for (int k = 0; k < 16; ++k)
-                        if (sb + k < nsplit) acc = fmaf(tvalue(v[k]), __shfl(e, sb + k), acc);
+                            for (int k = 0; k < 16; ++k) v[k] = v0[k];
+                        } else {
+                            load_o(sb, end, v);
+                        }
+                        poll_o(sb, end, v);
+#pragma unroll
+                        for (int k = 0; k < 16; ++k)
+                            if (sb + k < end) acc = fmaf(tvalue(v[k]), __shfl(e, sb + k - sb64), acc);
+                    }
                 }
                 tstore(tatt + h * HD + lane, acc / Lsum, tg + T_ATT);
             }
@@ -1514,24 +1549,14 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
         float lg = 0.f;
         int lr = 0, nrow = 0;
         drain();
-        // int4 rows are software-pipelined: the next unit's lines are read from the ring before this
-        // unit is computed, hiding the LDS latency (they are released with the current ones, after
-        // the wave's reads of them).  Wider rows (bf16 4 lines, int8 2) would not fit the registers.
-        constexpr bool kPipe = WT == WType::INT4;
-        Row<WT> rr[kLmR];
-        if (kPipe && gw < VOCAB / kLmR)
-#pragma unroll
-            for (int i = 0; i < kLmR; ++i) take_row<WT>(sm, cs, wave, lane, lbad, rr[i]);
+        // Not software-pipelined: a unit's lines are taken, multiplied and released before the next unit's are
+        // read (the take-ahead form held the next unit's rows across the iteration, the pattern that gave
+        // layout-dependent wrong results in gate_up).
 #pragma unroll 1
         for (int u = gw; u < VOCAB / kLmR; u += NW) {
-            Row<WT> nr[kLmR];
-            if (!kPipe) {
+            Row<WT> rr[kLmR];
 #pragma unroll
-                for (int i = 0; i < kLmR; ++i) take_row<WT>(sm, cs, wave, lane, lbad, rr[i]);
-            } else if (u + NW < VOCAB / kLmR) {
-#pragma unroll
-                for (int i = 0; i < kLmR; ++i) take_row<WT>(sm, cs, wave, lane, lbad, nr[i]);
-            }
+            for (int i = 0; i < kLmR; ++i) take_row<WT>(sm, cs, wave, lane, lbad, rr[i]);
             float d[kLmR];
 #pragma unroll
             for (int i = 0; i < kLmR; ++i) {
@@ -1560,9 +1585,6 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
                 drain();  // nothing left pending for the hot path
                 nrow = 0;
             }
-            if constexpr (kPipe)
-#pragma unroll
-                for (int i = 0; i < kLmR; ++i) rr[i] = nr[i];
         }
         if (lane < nrow) *glob(p.logits + lr) = lg;
         if (lane == 0) {
@@ -1636,21 +1658,22 @@ int decode_max_grid(WType wt) {
 }
 
 void launch_decode(WType wt, const DecodeParams& p, int grid, hipStream_t s) {
-    CLLM_REQUIRE(grid >= kDecodeMinGrid && grid <= kDecodeMaxGrid, "decode: grid must be 64..4096 workgroups");
-    CLLM_REQUIRE(p.max_seq > 0 && p.max_seq % kAttnChunk == 0 && p.max_seq <= 64 * kAttnChunk,
-                 "decode: max_seq must be a multiple of 128 and at most 8192");
+    CLLM_REQUIRE(grid >= kDecodeMinGrid && grid <= kDecodeMaxGrid && grid % 8 == 0,
+                 "decode: grid must be a multiple of 8 in 64..4096 workgroups");
+    CLLM_REQUIRE(p.max_seq > 0 && p.max_seq % kAttnChunk == 0 && p.max_seq <= kDecodeMaxSeq,
+                 "decode: max_seq must be a multiple of 128 and at most 131072");
+    // A cooperative launch: the runtime either makes every workgroup co-resident or refuses the launch
+    // (hipErrorCooperativeLaunchTooLarge), so the cross-workgroup waits never depend on workgroups that
+    // have not been scheduled.
+    DecodeParams arg = p;
+    void* args[] = {&arg};
+    const void* fn = nullptr;
     switch (wt) {
-        case WType::BF16:
-            hipLaunchKernelGGL(dk::decode_kernel<WType::BF16>, dim3(grid), dim3(kDecodeThreads), 0, s, p);
-            break;
-        case WType::INT8:
-            hipLaunchKernelGGL(dk::decode_kernel<WType::INT8>, dim3(grid), dim3(kDecodeThreads), 0, s, p);
-            break;
-        case WType::INT4:
-            hipLaunchKernelGGL(dk::decode_kernel<WType::INT4>, dim3(grid), dim3(kDecodeThreads), 0, s, p);
-            break;
+        case WType::BF16: fn = reinterpret_cast<const void*>(&dk::decode_kernel<WType::BF16>); break;
+        case WType::INT8: fn = reinterpret_cast<const void*>(&dk::decode_kernel<WType::INT8>); break;
+        case WType::INT4: fn = reinterpret_cast<const void*>(&dk::decode_kernel<WType::INT4>); break;
     }
-    CLLM_HIP(hipGetLastError());
+    CLLM_HIP(hipLaunchCooperativeKernel(fn, dim3(grid), dim3(kDecodeThreads), args, 0, s));
 }
 
 }  // namespace cllm

@@ -8,7 +8,11 @@ import ctypes
 
 import numpy as np
 
-from .engine import _check, _lib
+from .engine import call
+
+
+def _ptr(a: np.ndarray, ctype):
+    return a.ctypes.data_as(ctypes.POINTER(ctype))
 
 
 def quantize_int8_rows(w: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
@@ -16,9 +20,8 @@ def quantize_int8_rows(w: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
     rows, cols = w.shape
     q = np.empty((rows, cols), dtype=np.int8)
     s = np.empty(rows, dtype=np.float32)
-    _check(_lib().cudallm_quantize_int8_rows(w.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), rows, cols,
-                                             q.ctypes.data_as(ctypes.POINTER(ctypes.c_byte)),
-                                             s.ctypes.data_as(ctypes.POINTER(ctypes.c_float))))
+    call("cudallm_quantize_int8_rows", _ptr(w, ctypes.c_float), rows, cols, _ptr(q, ctypes.c_byte),
+         _ptr(s, ctypes.c_float))
     return q, s
 
 
@@ -31,9 +34,8 @@ def quantize_int4_groups(w: np.ndarray, group: int = 128) -> tuple[np.ndarray, n
     rows, cols = w.shape
     packed = np.empty((rows, cols // 2), dtype=np.uint8)
     s = np.empty((rows, cols // group), dtype=np.uint16)
-    _check(_lib().cudallm_quantize_int4_groups(w.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), rows, cols, group,
-                                               packed.ctypes.data_as(ctypes.POINTER(ctypes.c_ubyte)),
-                                               s.ctypes.data_as(ctypes.POINTER(ctypes.c_ushort))))
+    call("cudallm_quantize_int4_groups", _ptr(w, ctypes.c_float), rows, cols, group, _ptr(packed, ctypes.c_ubyte),
+         _ptr(s, ctypes.c_ushort))
     return packed, s.view(np.float16)
 
 
@@ -41,8 +43,7 @@ def unpack_int4(packed: np.ndarray) -> np.ndarray:
     packed = np.ascontiguousarray(packed, dtype=np.uint8)
     rows, half = packed.shape
     q = np.empty((rows, half * 2), dtype=np.int8)
-    _check(_lib().cudallm_unpack_int4(packed.ctypes.data_as(ctypes.POINTER(ctypes.c_ubyte)), rows, half * 2,
-                                      q.ctypes.data_as(ctypes.POINTER(ctypes.c_byte))))
+    call("cudallm_unpack_int4", _ptr(packed, ctypes.c_ubyte), rows, half * 2, _ptr(q, ctypes.c_byte))
     return q
 
 

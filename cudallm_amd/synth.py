@@ -4,7 +4,7 @@ The tensor list is the one the reference's exporter writes (``python/cudallm/exp
 fused ``wqkv`` (q|k|v rows) and ``w_gate_up`` (gate|up rows), tied embeddings, Llama-3 scaled
 ``rope.inv_freq``.  Every linear and the embedding is a bf16 master drawn N(0, 0.02) with torch's
 generator on the GPU; int8 / int4 files quantise that master (upcast to fp32, as ``export.py:90``
-does) with the GPU quantisers of this package.  Norm weights are 1.0 (HF initialisation).
+does) with the GPU quantisers of this package.  Norm weights are 1.0 (HF initialisation) or seeded U(0.5, 1.5).
 The file is streamed tensor by tensor, so host memory stays bounded by the largest tensor.
 """
 import math
@@ -59,12 +59,18 @@ def _specs(wdtype: str, d: dict) -> list[tuple[str, int, int, int]]:
     return s
 
 
-def write_model(path, wdtype: str, seed: int = 0, device: str | None = None, max_seq_len: int | None = None) -> int:
+def write_model(path, wdtype: str, seed: int = 0, device: str | None = None, max_seq_len: int | None = None,
+                norm: str = "ones") -> int:
     """Write a seeded Llama-3.2-1B-shaped model; returns the file's weight bytes (sum of nbytes).
 
     The bf16 master depends only on ``seed`` (and the device's generator), not on ``wdtype``.
     ``max_seq_len`` (default 4096) is the header's context limit; the weights do not depend on it.
+    ``norm``: "ones" (HF initialisation) or "random" (U(0.5, 1.5) from a numpy generator seeded with ``seed``,
+    so that a test can tell the norm weights of different layers apart).
     """
+    if norm not in ("ones", "random"):
+        raise ValueError("norm must be 'ones' or 'random'")
+    norm_rng = np.random.default_rng(seed)
     if wdtype not in ("bf16", "int8", "int4"):
         raise ValueError("wdtype must be bf16, int8 or int4")
     d = dict(LLAMA_1B)
@@ -84,7 +90,12 @@ def write_model(path, wdtype: str, seed: int = 0, device: str | None = None, max
     while i < len(specs):
         name, dtype, rows, cols = specs[i]
         if dtype == fmt.F32:
-            a = llama3_inv_freq(d["head_dim"], d["rope_theta"]) if name == "rope.inv_freq" else np.ones(rows, np.float32)
+            if name == "rope.inv_freq":
+                a = llama3_inv_freq(d["head_dim"], d["rope_theta"])
+            elif norm == "random":
+                a = norm_rng.uniform(0.5, 1.5, rows).astype(np.float32)
+            else:
+                a = np.ones(rows, np.float32)
             w.write(a.tobytes())
             total += a.nbytes
             i += 1

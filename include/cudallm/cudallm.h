@@ -82,6 +82,20 @@ int  cudallm_step_debug(cudallm_engine* e, int token, float* residuals_out, floa
 int  cudallm_step_profile(cudallm_engine* e, int token, unsigned long long* stamps_out, long long capacity,
                           int* grid_out);
 
+/* One decode step of the persistent kernel (synchronous, like cudallm_step_debug) that also returns
+ * every vector its phases exchanged.  No reference counterpart: the reference's test hooks check each
+ * kernel alone (tests/test_kernels.py); this lets a test check each phase of the fused kernel the same
+ * way, from that phase's own inputs.  trace_out receives, in floats:
+ *   [0, (L+1)*H)            the residual stream entering each layer, then after the last layer;
+ *   then L * (nh+2*nkv)*hd  per layer q and k after RoPE, then v (the qkv phase's output);
+ *   then L * nh*hd          per layer the attention output (after the split merge);
+ *   then L * H              per layer the residual after attention (x + Wo att);
+ *   then L * inter          per layer the SwiGLU output silu(gate) * up;
+ * capacity >= that total.  logits_out / next_token_out as for cudallm_step.  CUDALLM_ERR_STATE if the
+ * engine's options do not select the persistent kernel. */
+int  cudallm_step_trace(cudallm_engine* e, int token, float* trace_out, long long capacity, float* logits_out,
+                        int* next_token_out);
+
 /* The HIP stream (a hipStream_t) on which the engine enqueues every step.  No reference
  * counterpart (the reference's stream is private to its Engine, src/engine/engine.cpp:40): it lets
  * a caller order its own device work after the engine's, or time steps with HIP events recorded
@@ -123,6 +137,12 @@ int cudallm_launch_matvec(int weight_dtype, int epilogue, int rpb, const void* w
 int cudallm_launch_attention(const float* q, const unsigned short* k_cache, const unsigned short* v_cache,
                              const int* d_pos, float* part_o, float* part_ml, float* out, int nh, int nkv, int hd,
                              int max_seq, void* stream);
+
+/* Measured stream-read bandwidth of device memory (GB/s = 1e9 B/s): a `bytes` buffer (>= 64 MiB; use more than
+ * the 256 MB Infinity Cache, e.g. 4 GiB) read `reps` times after warm-up for each of a few launch shapes; the best
+ * and the median of the best shape.  No reference counterpart in C: the reference measures the same quantity with
+ * its tool src/tools/cudallm_bandwidth.cpp:19-68 ("read_gbps_best", the peak its roofline fractions use). */
+int cudallm_measure_read_bandwidth(unsigned long long bytes, int reps, double* best_gbps, double* median_gbps);
 
 /* ---- weight quantisers on the GPU (no reference counterpart in C) ----
  * They replace the reference's offline numpy quantisers, python/cudallm/quantize.py:5-38, with

@@ -47,3 +47,26 @@ def model_dir(tmp_path_factory):
         Path(d).mkdir(parents=True, exist_ok=True)
         return Path(d)
     return tmp_path_factory.mktemp("models")
+
+
+# The engine tests' model files: seeded Llama-3.2-1B-shaped weights with random norm weights (so a
+# wrong norm index shows) and a header that allows 16384 positions (contexts past 8192).
+TEST_MODEL_SEED = 1234
+TEST_MODEL_MAX_SEQ = 16384
+
+
+@pytest.fixture(scope="session")
+def model_path(gpu, model_dir):
+    """model_path(wd) -> path of the shared test model for weight type wd, written on first use."""
+    from cudallm_amd import synth
+    cache = {}
+
+    def get(wd):
+        if wd not in cache:
+            p = model_dir / f"synth_seed{TEST_MODEL_SEED}_{wd}_norm_ms{TEST_MODEL_MAX_SEQ}.cudallm"
+            if not p.exists():
+                print(f"[model] writing {p}", flush=True)
+                synth.write_model(p, wd, seed=TEST_MODEL_SEED, max_seq_len=TEST_MODEL_MAX_SEQ, norm="random")
+            cache[wd] = p
+        return cache[wd]
+    return get

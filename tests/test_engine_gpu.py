@@ -11,7 +11,6 @@ import numpy as np
 import pytest
 
 from cudallm_amd import engine as E
-from cudallm_amd import synth
 from oracle.model import OracleModel
 
 pytestmark = [pytest.mark.gpu, pytest.mark.timeout(900)]
@@ -33,21 +32,6 @@ def _id(c):
 
 def _threads() -> int:
     return min(16, os.cpu_count() or 1)
-
-
-@pytest.fixture(scope="module")
-def model_path(gpu, model_dir):
-    cache = {}
-
-    def get(wd):
-        if wd not in cache:
-            p = model_dir / f"synth_seed1234_{wd}.cudallm"
-            if not p.exists():
-                print(f"[engine] writing {p}", flush=True)
-                synth.write_model(p, wd, seed=1234)
-            cache[wd] = p
-        return cache[wd]
-    return get
 
 
 @pytest.fixture(scope="module")
@@ -91,7 +75,8 @@ def engine_runs(model_path):
         if cfg not in cache:
             wd, mv, at, fuse, graph = cfg
             print(f"[engine] run {_id(cfg)}", flush=True)
-            with E.Engine(model_path(wd), matvec=mv, attn=at, fuse=bool(fuse), cuda_graph=bool(graph)) as eng:
+            with E.Engine(model_path(wd), matvec=mv, attn=at, fuse=bool(fuse), cuda_graph=bool(graph),
+                          max_seq_len=4096) as eng:
                 logits, res, nexts = _run(eng, TOKENS, graph)
                 eng.reset()
                 rerun, _, _ = _run(eng, TOKENS[:4], graph)
@@ -214,22 +199,23 @@ def test_sequence_full_and_token_range(model_path):
         assert eng.pos == 1 and nxt == int(np.argmax(lg))
 
 
-@pytest.mark.parametrize("wd", ["int4", "bf16"])
+@pytest.mark.parametrize("wd", ["bf16", "int8", "int4"])
 def test_persistent_long_context_matches_multikernel(wd, model_path, monkeypatch):
-    """Contexts past one 128-token chunk: the persistent kernel's split-K attention and its LSE merge
-    (up to 6 splits here) against the multi-kernel path, whose split-K attention kernels are checked
-    against the float64 oracle up to context 8192 in test_kernels_gpu.py.  Both engines are
-    teacher-forced with the same tokens to context 700."""
-    steps = 700
+    """Contexts to 8000 (the long suite's context, 63 splits): the persistent kernel's split-K attention and LSE
+    merge against the multi-kernel path, whose split-K attention kernels are checked against the float64 oracle
+    up to context 8192 in test_kernels_gpu.py.  Both engines are teacher-forced with the same tokens; logits are
+    compared at the split boundaries and every 250 positions."""
+    steps = 8000
     monkeypatch.setenv("CUDALLM_PERSISTENT", "0")
-    ref = E.Engine(model_path(wd), max_seq_len=1024)
+    ref = E.Engine(model_path(wd), max_seq_len=8192)
     monkeypatch.delenv("CUDALLM_PERSISTENT")
-    eng = E.Engine(model_path(wd), max_seq_len=1024)
+    eng = E.Engine(model_path(wd), max_seq_len=8192)
+    boundary = {127, 128, 129, 255, 256, 257, 1023, 1024, 4095, 4096, 7999}
     try:
         toks = [128000]
         worst, agree, checked = 0.0, 0, 0
         for i in range(steps):
-            check = i % 25 == 24 or i in (127, 128, 129, 511, 512, 513)
+            check = i % 250 == 249 or i in boundary
             n_ref, lg_ref = ref.step(toks[-1], want_logits=check)
             n_eng, lg_eng = eng.step(toks[-1], want_logits=check)
             if check:
@@ -268,7 +254,7 @@ def test_stalls_leave_results_bit_identical(wd, model_path, engine_runs, monkeyp
     for name, mask in STALLS.items():
         monkeypatch.setenv("CUDALLM_STALL", hex(mask))
         try:
-            with E.Engine(model_path(wd), cuda_graph=False) as eng:
+            with E.Engine(model_path(wd), cuda_graph=False, max_seq_len=4096) as eng:
                 logits, res, _ = _run(eng, TOKENS[:8], graph=False)
         finally:
             monkeypatch.delenv("CUDALLM_STALL")
