@@ -83,6 +83,33 @@ def bench_decode(path, wd: str, steps: int, warmup: int, torch) -> dict:
             "last_token": nxt, "kernel_avg_us": ev_us, "kernel_gbps": bpt / ev_us / 1e3}
 
 
+def bench_config5(path, reps: int = 5, warmup: int = 1, prompt: int = PROMPT, gen: int = 256) -> dict:
+    """BASELINE config 5 timed the way reference src/tools/cudallm_bench.cpp:64-85 times it: per rep, reset, the
+    prompt, a drained stream, then `gen` greedy steps (token -1, no host sync) timed to the drained end; the median
+    tok/s over `reps` reps after `warmup` untimed reps.  Bytes per token = weight bytes + 32768 (prompt + ceil(gen/2))."""
+    from cudallm_amd import engine as E
+    ids = prompt_ids(prompt)
+    rates = []
+    with E.Engine(path, max_seq_len=4096) as eng:
+        weight_bytes = eng.config["weight_bytes"]
+        for r in range(warmup + reps):
+            eng.reset()
+            for t in ids[:-1]:
+                eng.step_async(t)
+            eng.step(ids[-1])  # the last prompt step returns its output, so the stream is drained here
+            t0 = time.perf_counter()
+            for _ in range(gen - 1):
+                eng.step_async(None)
+            eng.step(None)  # the gen-th greedy step, and the drain
+            dt = time.perf_counter() - t0
+            if r >= warmup:
+                rates.append(gen / dt)
+    bpt = weight_bytes + KV_BYTES_PER_POS * (prompt + (gen + 1) // 2)
+    med = float(np.median(rates))
+    return {"tok_s": med, "reps": reps, "prompt": prompt, "gen": gen, "bytes_per_token": bpt,
+            "gbps": bpt * med / 1e9, "frac_of_8tbs": bpt * med / PEAK_HBM, "all_tok_s": [round(r, 2) for r in rates]}
+
+
 TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic.json"
 
 
@@ -127,8 +154,21 @@ def cpu_baseline(path, budget_s: float) -> dict:
     dt = time.perf_counter() - t0
     return {"value": n / dt, "unit": "tok/s", "cores": torch.get_num_threads(), "kind": "port",
             "sample": f"{n} bf16 decode steps (positions 1..{n}) of the same synthetic model by the oracle "
-                      f"(torch fp32 on the host, weights dequantised per matmul), {dt:.1f} s; "
-                      f"os.cpu_count()={os.cpu_count()}"}
+                      f"(torch fp32 on the host, weights dequantised per matmul), {dt:.1f} s",
+            "host": host_description()}
+
+
+def host_description() -> dict:
+    """The host the CPU baseline ran on: core counts and the CPU model."""
+    model = None
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"os_cpu_count": os.cpu_count(), "sched_getaffinity": len(os.sched_getaffinity(0)), "cpu_model": model}
 
 
 def cpu_matvec_config1(reps: int = 20) -> dict:
@@ -159,6 +199,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-kernels", action="store_true", help="skip the per-shape matvec lines")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-config5", action="store_true", help="skip the config-5 sequence leg")
+    ap.add_argument("--no-peak", action="store_true", help="skip the measured stream-read peak")
     ap.add_argument("--model-dir", default=None)
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="first run three device copies of MIB MiB (byte-counter calibration under rocprofv3)")
@@ -180,6 +222,14 @@ def main() -> int:
     if args.copy_calib:
         copy_calibration(args.copy_calib, torch)
     dtypes = [d for d in args.dtypes.split(",") if d]
+    peak = None
+    if not args.no_peak:
+        from cudallm_amd import engine as E
+        best, med = E.measure_read_bandwidth(4 << 30, 10)
+        peak = {"best_gbps": round(best, 1), "median_gbps": round(med, 1), "bytes": 4 << 30,
+                "method": "stream read of a 4 GiB buffer (> the 256 MB Infinity Cache), best of 10 timed reads "
+                          "over a sweep of launch shapes (cudallm_measure_read_bandwidth)"}
+        log(f"[bench] measured HBM stream-read peak: best {best:.0f} GB/s, median {med:.0f} GB/s")
     base = args.model_dir or ("/dev/shm" if os.path.isdir("/dev/shm") else None)
     tmp = tempfile.TemporaryDirectory(dir=base)
     paths = {}
@@ -193,13 +243,19 @@ def main() -> int:
         log(f"[bench] decode {wd}: {decode[wd]['tok_s']:.1f} tok/s, {decode[wd]['gbps']:.0f} GB/s "
             f"({100 * decode[wd]['frac_of_8tbs']:.1f} % of 8 TB/s); kernel {decode[wd]['kernel_avg_us']:.1f} us "
             f"by events")
+        if not args.no_config5:
+            decode[wd]["config5"] = bench_config5(paths[wd])
+            c5 = decode[wd]["config5"]
+            log(f"[bench] config 5 {wd} (16 + 256, median of {c5['reps']}): {c5['tok_s']:.1f} tok/s, "
+                f"{100 * c5['frac_of_8tbs']:.1f} % of 8 TB/s")
         if wd != "bf16" or args.no_cpu:
             paths[wd].unlink()
 
     head_wd = "bf16" if "bf16" in dtypes else dtypes[0]
     dom = bench_matvec(head_wd, "gate_up", 16384, 2048, "swiglu", True, 400)
     dom_gbps = dom["bytes"] / dom["avg_us"] / 1e3
-    log(f"[bench] gate_up {head_wd} matvec: {dom['avg_us']:.2f} us, {dom_gbps:.0f} GB/s")
+    log(f"[bench] gate_up {head_wd} matvec: kernel {dom['avg_us']:.2f} us, {dom_gbps:.0f} GB/s "
+        f"(wall {dom['wall_us_per_launch']:.2f} us per launch)")
     matvecs = []
     if not args.no_kernels:
         for wd in dtypes:
@@ -220,6 +276,16 @@ def main() -> int:
     tmp.cleanup()
 
     head = decode[head_wd]
+    pk = peak["best_gbps"] if peak else None
+    for r in decode.values():
+        if pk:
+            r["frac_of_measured_peak"] = r["gbps"] / pk
+            r["kernel_frac_of_measured_peak"] = r["kernel_gbps"] / pk
+            if "config5" in r:
+                r["config5"]["frac_of_measured_peak"] = r["config5"]["gbps"] / pk
+    for r in matvecs:
+        if pk and "bytes" in r:
+            r["frac_of_measured_peak"] = r["bytes"] / r["avg_us"] / 1e3 / pk
     rec = {
         "metric": METRIC, "value": round(head["tok_s"], 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(head["ms_per_token"], 4), "higher_is_better": True,
@@ -234,10 +300,15 @@ def main() -> int:
                      "kernel": f"decode_kernel<{head_wd}> (persistent: the whole decode step is this one launch)",
                      "bytes_per_launch": head["bytes_per_token"], "avg_us": round(head["kernel_avg_us"], 3),
                      "timing": "HIP events on the engine's stream around the timed steps",
-                     "traffic_source": TRAFFIC_FILE.name},
+                     "traffic_source": TRAFFIC_FILE.name,
+                     "measured_peak": pk, "frac_of_measured_peak": round(head["kernel_gbps"] / pk, 4) if pk else None},
+        "hbm_read_peak": peak,
         "matvec_roofline": {"kernel": f"matvec_fast<{head_wd}, SWIGLU, norm> gate_up 16384x2048 (standalone)",
                             "achieved": round(dom_gbps, 1), "frac": round(dom["frac_of_8tbs"], 4),
-                            "bytes_per_launch": dom["bytes"], "avg_us": round(dom["avg_us"], 3)},
+                            "frac_of_measured_peak": round(dom_gbps / pk, 4) if pk else None,
+                            "bytes_per_launch": dom["bytes"], "avg_us": round(dom["avg_us"], 3),
+                            "timing": "mean kernel duration from dispatch-recorded start/end events, "
+                                      "rotating over > 1.5 GiB of weight copies"},
         "cpu_baseline": cpu,
         "decode": {wd: {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
                    for wd, r in decode.items()},

@@ -127,6 +127,18 @@ private:
     void* dev_ = nullptr;
 };
 
+// The opt matvec on device pointers: shared by the plain and the timed launch entry points.
+void enqueue_matvec(int weight_dtype, int epilogue, int rpb, const void* w, const void* scales, const float* x,
+                    const float* norm_w, float eps, float* y, int rows, int cols, void* stream) {
+    const cllm::WType wt = weight_type(weight_dtype);
+    need(epilogue == 0 || epilogue == 1 || epilogue == 2, "epilogue must be 0, 1 or 2");
+    need(rpb == 0 || rpb == 1 || rpb == 2 || rpb == 4 || rpb == 8, "rpb must be 0, 1, 2, 4 or 8");
+    need(wt != cllm::WType::INT4 || cols % 128 == 0, "int4 weights need cols to be a multiple of 128");
+    const cllm::MatvecArgs a{w, scales, x, norm_w, eps, y, rows, cols};
+    cllm::launch_matvec(wt, static_cast<cllm::Epilogue>(epilogue), a, rpb ? rpb : cllm::default_rpb(wt),
+                        static_cast<hipStream_t>(stream));
+}
+
 }  // namespace
 
 extern "C" {
@@ -369,13 +381,20 @@ int cudallm_kernel_argmax(const float* logits, int n, int* out_idx) {
 int cudallm_launch_matvec(int weight_dtype, int epilogue, int rpb, const void* w, const void* scales, const float* x,
                           const float* norm_w, float eps, float* y, int rows, int cols, void* stream) {
     return abi_entry("cudallm_launch_matvec", [&] {
-        const cllm::WType wt = weight_type(weight_dtype);
-        need(epilogue == 0 || epilogue == 1 || epilogue == 2, "epilogue must be 0, 1 or 2");
-        need(rpb == 0 || rpb == 1 || rpb == 2 || rpb == 4 || rpb == 8, "rpb must be 0, 1, 2, 4 or 8");
-        need(wt != cllm::WType::INT4 || cols % 128 == 0, "int4 weights need cols to be a multiple of 128");
-        const cllm::MatvecArgs a{w, scales, x, norm_w, eps, y, rows, cols};
-        cllm::launch_matvec(wt, static_cast<cllm::Epilogue>(epilogue), a, rpb ? rpb : cllm::default_rpb(wt),
-                            static_cast<hipStream_t>(stream));
+        enqueue_matvec(weight_dtype, epilogue, rpb, w, scales, x, norm_w, eps, y, rows, cols, stream);
+    });
+}
+
+int cudallm_launch_matvec_timed(int weight_dtype, int epilogue, int rpb, const void* w, const void* scales,
+                                const float* x, const float* norm_w, float eps, float* y, int rows, int cols,
+                                void* stream, void* start_event, void* stop_event) {
+    return abi_entry("cudallm_launch_matvec_timed", [&] {
+        need(start_event && stop_event, "start_event and stop_event are required");
+        struct Disarm {  // the events never stay armed for a later launch, also when this one is refused
+            ~Disarm() { cllm::take_kernel_events(); }
+        } disarm;
+        cllm::arm_kernel_events(static_cast<hipEvent_t>(start_event), static_cast<hipEvent_t>(stop_event));
+        enqueue_matvec(weight_dtype, epilogue, rpb, w, scales, x, norm_w, eps, y, rows, cols, stream);
     });
 }
 

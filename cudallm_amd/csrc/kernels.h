@@ -24,6 +24,13 @@ struct MatvecArgs {
 };
 
 int default_rpb(WType wt);
+// Events the next matvec launch on this thread records at its kernel's start and end (benchmarks: the interval
+// excludes the launch gap).  take_kernel_events() returns and clears them.
+struct KernelEvents {
+    hipEvent_t start = nullptr, stop = nullptr;
+};
+void arm_kernel_events(hipEvent_t start, hipEvent_t stop);
+KernelEvents take_kernel_events();
 // y (= | +=) W x^ with the selected epilogue; x^ = rmsnorm(x) * norm_w when norm_w != null.
 void launch_matvec(WType wt, Epilogue ep, const MatvecArgs& a, int rpb, hipStream_t s);
 // One thread per row, bf16, STORE only: the deliberately uncoalesced ablation baseline.

@@ -34,6 +34,18 @@ int default_rpb(WType wt) {
     throw ArgError("unknown weight type");
 }
 
+namespace {
+thread_local KernelEvents t_kernel_events;
+}
+
+void arm_kernel_events(hipEvent_t start, hipEvent_t stop) { t_kernel_events = {start, stop}; }
+
+KernelEvents take_kernel_events() {
+    const KernelEvents e = t_kernel_events;
+    t_kernel_events = {};
+    return e;
+}
+
 template <WType WT>
 void launch_matvec_wt(Epilogue ep, const MatvecArgs& a, int rpb, hipStream_t s);
 

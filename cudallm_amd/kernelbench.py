@@ -39,8 +39,10 @@ def matvec_bytes(wd: str, rows: int, cols: int) -> int:
 
 def bench_matvec(wd: str, name: str, rows: int, cols: int, ep: str, norm: bool, iters: int, rpb: int = 0,
                  rotate_bytes: float = 1.5 * (1 << 30)) -> dict:
-    """Time `iters` launches with HIP events around each one, on torch's current stream, rotating over weight copies
-    totalling at least `rotate_bytes`.  Returns the reference's fields plus the mean (avg_us) and the copy count."""
+    """Time `iters` launches on torch's current stream, rotating over weight copies totalling at least `rotate_bytes`.
+    Each kernel's duration comes from events its own dispatch records at the kernel's start and end.  Returns the
+    reference's fields (median_us, gbps) plus the mean kernel time (avg_us), the wall time per launch including the
+    launch gap, and the copy count."""
     import torch
     from . import engine as E
     dev = torch.device("cuda")
@@ -66,27 +68,36 @@ def bench_matvec(wd: str, name: str, rows: int, cols: int, ep: str, norm: bool, 
     stream = torch.cuda.current_stream()
     sp = stream.cuda_stream
 
-    def launch(i):
+    def launch(i, ev=None):
         w, s = ws[i % copies], ss[i % copies]
-        E.launch_matvec(wd, ep, rpb, w.data_ptr(), s.data_ptr() if s is not None else None, x.data_ptr(),
-                        nw.data_ptr() if norm else None, 1e-5, y.data_ptr(), rows, cols, sp)
+        args = (wd, ep, rpb, w.data_ptr(), s.data_ptr() if s is not None else None, x.data_ptr(),
+                nw.data_ptr() if norm else None, 1e-5, y.data_ptr(), rows, cols, sp)
+        if ev is None:
+            E.launch_matvec(*args)
+        else:
+            E.launch_matvec_timed(*args, ev[0].cuda_event, ev[1].cuda_event)
 
     for i in range(min(copies, 20)):
         launch(i)
     torch.cuda.synchronize()
-    evs = [torch.cuda.Event(enable_timing=True) for _ in range(iters + 1)]
-    evs[0].record(stream)
+    # Kernel time: events recorded by each dispatch at its kernel's start and end (no launch gap), as a
+    # profiler's kernel trace reports it.  Wall time: events between consecutive launches (gaps included).
+    kev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(iters)]
+    w0, w1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    w0.record(stream)
     for i in range(iters):
-        launch(i)
-        evs[i + 1].record(stream)
-    evs[-1].synchronize()
-    per = [evs[i].elapsed_time(evs[i + 1]) * 1e3 for i in range(iters)]
-    med, avg = statistics.median(per), evs[0].elapsed_time(evs[-1]) * 1e3 / iters
+        launch(i, kev[i])
+    w1.record(stream)
+    w1.synchronize()
+    per = [a.elapsed_time(b) * 1e3 for a, b in kev]
+    med, avg = statistics.median(per), statistics.fmean(per)
+    wall = w0.elapsed_time(w1) * 1e3 / iters
     del ws, ss
     torch.cuda.empty_cache()
     return {"name": name, "rows": rows, "cols": cols, "impl": "opt", "wtype": wd, "epilogue": ep, "fuse_norm": norm,
             "rpb": rpb or DEFAULT_RPB[wd], "bytes": nbytes, "median_us": med, "gbps": nbytes / med / 1e3,
-            "avg_us": avg, "frac_of_8tbs": nbytes / avg / 1e3 / PEAK_GBPS, "copies": copies}
+            "avg_us": avg, "frac_of_8tbs": nbytes / avg / 1e3 / PEAK_GBPS, "wall_us_per_launch": wall,
+            "copies": copies, "timing": "kernel start/end events recorded by the dispatch (hipExtLaunchKernel)"}
 
 
 def weighted_us(per_shape_us: dict) -> float:

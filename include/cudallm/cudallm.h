@@ -132,6 +132,12 @@ int cudallm_kernel_argmax(const float* logits, int n, int* out_idx);
 /* Same operands and epilogues as cudallm_kernel_matvec (opt kernel); norm_w != NULL fuses RMSNorm. */
 int cudallm_launch_matvec(int weight_dtype, int epilogue, int rpb, const void* w, const void* scales,
                           const float* x, const float* norm_w, float eps, float* y, int rows, int cols, void* stream);
+/* cudallm_launch_matvec whose kernel records start_event / stop_event (hipEvent_t, created by the caller) at its
+ * own start and end (hipExtLaunchKernel), so hipEventElapsedTime gives the kernel's duration without the launch
+ * gap: what a profiler's kernel trace reports.  For kernel benchmarks. */
+int cudallm_launch_matvec_timed(int weight_dtype, int epilogue, int rpb, const void* w, const void* scales,
+                                const float* x, const float* norm_w, float eps, float* y, int rows, int cols,
+                                void* stream, void* start_event, void* stop_event);
 /* Split-K GQA attention over ctx = *d_pos + 1 tokens; part_o holds nh*(max_seq/128)*hd floats and
  * part_ml nh*(max_seq/128)*2 floats of scratch. */
 int cudallm_launch_attention(const float* q, const unsigned short* k_cache, const unsigned short* v_cache,
