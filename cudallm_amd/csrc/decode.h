@@ -56,6 +56,9 @@ struct DecodeParams {
     // input, kStallLoader makes each loader wave sleep at every segment switch, and kStallOdd limits
     // the sleeps to odd workgroups.  Results must stay bit-identical under any mask.
     unsigned stall;
+    // Co-residency probe (engine set-up only, null in a decode step): every workgroup adds 1 to probe[0] and waits,
+    // with a bound, until all gridDim.x have arrived; a workgroup that gives up sets probe[1].  Nothing else runs.
+    unsigned* probe;
 };
 
 enum : unsigned {
@@ -88,8 +91,12 @@ constexpr int kDecodeMaxSeq = 131072;
 // host clears every tagged buffer and restarts the counter before it gets there.
 constexpr unsigned kDecodeStepLimit = (1u << 24) - 2;
 
-// Enqueue one decode step (one cooperative launch: every workgroup is co-resident or the launch fails).
+// Enqueue one decode step: one plain launch of `grid` workgroups, which must all be co-resident (the engine checks
+// that once with a probe launch, decode_grid_is_resident; every cross-workgroup wait is bounded besides).
 void launch_decode(WType wt, const DecodeParams& p, int grid, hipStream_t s);
+// Launches the decode kernel in probe mode with `grid` workgroups and reports whether all of them were resident at
+// once.  `probe` is two zeroed device words.
+bool decode_grid_is_resident(WType wt, const DecodeParams& p, int grid, unsigned* probe, hipStream_t s);
 // Workgroups of the decode kernel that fit on the device at once for this weight type.
 int decode_max_grid(WType wt);
 

@@ -1,7 +1,8 @@
 // Decode engine.  What a step computes is the op order of reference src/engine/engine.cpp:181-237; how
 // it is run is this file's own:
 //
-//  * Default options: the persistent decode kernel, one cooperative launch per token.  Its
+//  * Default options: the persistent decode kernel, one launch per token (its workgroups' co-residency is
+//    verified once, at construction, by a probe launch).  Its
 //    cross-workgroup handoffs are tagged words (decode.h) whose epochs the host restarts before the
 //    32-bit tags could repeat.
 //  * Ablation options: a step program, the list of kernel launches of one step in op order, built
@@ -116,16 +117,13 @@ Engine::Engine(const std::string& path, const EngineOptions& opts) : opts_(opts)
         const size_t H = c.hidden, I = c.inter, V = c.vocab, S = max_seq_, KV = c.n_kv_heads, D = c.head_dim,
                      NH = c.n_heads, L = c.n_layers, NS = S / kAttnChunk, QKV = (NH + 2 * KV) * D;
 
-        // The persistent kernel needs: the default options, a cooperative launch of one workgroup per CU
-        // with the grid a multiple of 8, and a context it supports.  CUDALLM_PERSISTENT=0 selects the
-        // multi-kernel step instead (for comparisons).
-        int dev = 0, coop = 0;
-        CLLM_HIP(hipGetDevice(&dev));
-        CLLM_HIP(hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev));
+        // The persistent kernel needs: the default options, one workgroup per CU with the grid a multiple of 8,
+        // all of them resident at once (checked below with a probe launch), and a context it supports.
+        // CUDALLM_PERSISTENT=0 selects the multi-kernel step instead (for comparisons).
         const char* env = std::getenv("CUDALLM_PERSISTENT");
         const bool wanted = opts_.fuse && opts_.matvec == 1 && opts_.attn == 1 && !(env && !std::strcmp(env, "0"));
         grid_ = device_cu_count();
-        persistent_ = wanted && coop && S <= static_cast<size_t>(kDecodeMaxSeq) && grid_ % 8 == 0 &&
+        persistent_ = wanted && S <= static_cast<size_t>(kDecodeMaxSeq) && grid_ % 8 == 0 &&
                       grid_ >= kDecodeMinGrid && grid_ <= kDecodeMaxGrid && decode_max_grid(c.wt) >= grid_;
 
         ArenaPlan ap;
@@ -145,7 +143,7 @@ Engine::Engine(const std::string& path, const EngineOptions& opts) : opts_(opts)
                      at_targ = ap.reserve<uint64_t>(2 * kDecodeMaxGrid);
         const size_t at_tags_end = ap.size();
         const size_t at_layers = ap.reserve<DecodeLayer>(L), at_step = ap.reserve<unsigned>(1),
-                     at_err = ap.reserve<unsigned>(1),
+                     at_err = ap.reserve<unsigned>(1), at_probe = ap.reserve<unsigned>(2),
                      at_stamps = ap.reserve<unsigned long long>(static_cast<size_t>(grid_) * kStampSlots);
         CLLM_HIP(hipMalloc(&arena_, ap.size()));
         CLLM_HIP(hipMemset(arena_, 0, ap.size()));
@@ -210,6 +208,15 @@ Engine::Engine(const std::string& path, const EngineOptions& opts) : opts_(opts)
         const char* stall = std::getenv("CUDALLM_STALL");  // timing perturbation, tests only
         dp_.stall = stall ? static_cast<unsigned>(std::strtoul(stall, nullptr, 0)) : 0u;
 
+        CLLM_HIP(hipDeviceSynchronize());
+        // Every workgroup of the persistent grid must be resident at once (their waits on each other would
+        // otherwise only end at their bounds).  One probe launch checks it for this device and kernel; if it
+        // fails (another process holding CUs, say), this engine runs the multi-kernel step instead.
+        if (persistent_ && !decode_grid_is_resident(c.wt, dp_, grid_, static_cast<unsigned*>(at(at_probe)), stream_)) {
+            std::fprintf(stderr, "cudallm: the %d workgroups of the persistent decode kernel were not all resident at "
+                                 "once; using the multi-kernel step\n", grid_);
+            persistent_ = false;
+        }
         if (!persistent_) build_program();
         CLLM_HIP(hipDeviceSynchronize());
     } catch (...) {
@@ -387,9 +394,8 @@ void Engine::read_outputs(float* logits_out, int* next_token_out) {
 
 void Engine::step(int token, float* logits_out, int* next_token_out) {
     begin_step("step", token);
-    // The persistent step is one kernel launched directly whether or not cuda_graph is set (a cooperative
-    // launch; replaying a one-node graph of it only adds launch latency).  The multi-kernel program is captured
-    // on first use and replayed.
+    // The persistent step is one kernel launched directly whether or not cuda_graph is set (replaying a one-node
+    // graph of it only adds launch latency).  The multi-kernel program is captured on first use and replayed.
     if (persistent_) {
         launch_persistent(dp_);
     } else if (opts_.graph) {

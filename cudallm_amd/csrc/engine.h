@@ -1,7 +1,7 @@
 // Batch-1 decode engine: owns the weights, the activations, the fp16 KV cache and the decode step.
 //
 // Two ways to run a step:
-//  * the persistent decode kernel (decode.h), one cooperative launch per token, for the default
+//  * the persistent decode kernel (decode.h), one launch per token, for the default
 //    options (opt matvec, opt attention, fused);
 //  * the multi-kernel step, for the reference's ablation options: a fixed program of kernel
 //    launches built once at construction, replayed from a captured hipGraph when cuda_graph is set.

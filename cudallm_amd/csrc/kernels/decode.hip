@@ -1010,6 +1010,54 @@ __device__ __forceinline__ void wave_argmax(float& v, int& i) {
 
 constexpr int kDppRor8 = 0x128;  // row_ror:8: lane i reads lane (i + 8) mod 16 of its 16-lane row
 
+// LSE merge for contexts past 64 splits (more than 8192 positions): one wave per head, the splits in blocks of 64
+// (lane s holds split sb + s).  Pass 1 takes the maximum over every block; pass 2 adds up l e^(m - M) per block
+// and the o values in split order.  Kept out of line: it is off the hot path, and inlined its state would
+// compete for the main loop's registers.
+__device__ __noinline__ void merge_long(const uint64_t* tpart, uint64_t* tatt, unsigned tg, int nsplit, int NS, int gw,
+                                        int NW, int lane, unsigned* err) {
+    const unsigned tag = tg + T_ATT_PART;
+    for (int h = gw; h < NH; h += NW) {
+        const uint64_t* pp = tpart + static_cast<size_t>(h) * NS * kPartStride;
+        auto poll_ml = [&](int sb, float& ms, float& ls) {
+            const bool in = sb + lane < nsplit;
+            uint64_t vm = static_cast<uint64_t>(tag) << 32, vl = vm;
+            if (in) {
+                vm = tload(pp + (sb + lane) * kPartStride + HD);
+                vl = tload(pp + (sb + lane) * kPartStride + HD + 1);
+            }
+            unsigned spins = 0;
+            while (!(tagged(vm, tag) && tagged(vl, tag)) && !give_up(spins, err)) {
+                if (!tagged(vm, tag)) vm = tload(pp + (sb + lane) * kPartStride + HD);
+                if (!tagged(vl, tag)) vl = tload(pp + (sb + lane) * kPartStride + HD + 1);
+            }
+            ms = in ? tvalue(vm) : -INFINITY;
+            ls = in ? tvalue(vl) : 0.f;
+        };
+        float M = -INFINITY;
+        for (int sb = 0; sb < nsplit; sb += kWave) {
+            float ms, ls;
+            poll_ml(sb, ms, ls);
+            M = fmaxf(M, wave_max(ms));
+        }
+        float Lsum = 0.f, acc = 0.f;
+        for (int sb64 = 0; sb64 < nsplit; sb64 += kWave) {
+            float ms, ls;
+            poll_ml(sb64, ms, ls);
+            const float e = sb64 + lane < nsplit ? expf(ms - M) : 0.f;
+            Lsum += wave_sum(ls * e);
+            const int end = min(nsplit, sb64 + kWave);
+            for (int sb = sb64; sb < end; ++sb) {
+                uint64_t v = tload(pp + sb * kPartStride + lane);
+                unsigned spins = 0;
+                while (!tagged(v, tag) && !give_up(spins, err)) v = tload(pp + sb * kPartStride + lane);
+                acc = fmaf(tvalue(v), __shfl(e, sb - sb64), acc);
+            }
+        }
+        tstore(tatt + h * HD + lane, acc / Lsum, tg + T_ATT);
+    }
+}
+
 // ---- the kernel ------------------------------------------------------------------------------
 
 template <WType WT>
@@ -1025,6 +1073,23 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
         sm.bar[threadIdx.x] = 0;
     }
     __syncthreads();  // the only workgroup-wide barrier: loaders never join another one
+    if (p.probe) {  // co-residency probe: arrive, wait (bounded) for every workgroup, leave
+        if (threadIdx.x == 0) {
+            __hip_atomic_fetch_add(glob(p.probe), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            unsigned spins = 0;
+            for (;;) {
+                const unsigned n = __hip_atomic_load(glob(p.probe), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const unsigned bad = __hip_atomic_load(glob(p.probe + 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (n >= gridDim.x || bad) break;
+                if (++spins >= kSpinCap) {
+                    __hip_atomic_store(glob(p.probe + 1), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(2);
+            }
+        }
+        return;
+    }
     {
         const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
         if (w >= kCW) {
@@ -1283,86 +1348,54 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
         }
         stamp(p, 1 + 6 * l + 1);
 
-        // ---- LSE merge of the splits: one wave per head, lane s holds split s of each 64-split block ----
+        // ---- LSE merge of the splits: one wave per head ----
         renew();
-        if (nsplit > 1) {
-            const unsigned tag = tg + T_ATT_PART;
+        if (nsplit > 1 && nsplit <= kWave) {
+            // Lane s holds split s; one round trip for the first 16 splits: each lane's (m, l) and the o values
+            // all in flight at once.
 #pragma unroll 1
             for (int h = gw; h < NH; h += NW) {
                 const uint64_t* pp = tpart + static_cast<size_t>(h) * NS * kPartStride;
-                // (m, l) of split sb + lane, polled until tagged; one round trip for the whole block.
-                auto poll_ml = [&](int sb, float& ms, float& ls) {
-                    const bool in = sb + lane < nsplit;
-                    uint64_t vm = static_cast<uint64_t>(tag) << 32, vl = vm;
-                    if (in) {
-                        vm = tload(pp + (sb + lane) * kPartStride + HD);
-                        vl = tload(pp + (sb + lane) * kPartStride + HD + 1);
-                    }
-                    unsigned spins = 0;
-                    while (!(tagged(vm, tag) && tagged(vl, tag)) && !give_up(spins, err)) {
-                        if (!tagged(vm, tag)) vm = tload(pp + (sb + lane) * kPartStride + HD);
-                        if (!tagged(vl, tag)) vl = tload(pp + (sb + lane) * kPartStride + HD + 1);
-                    }
-                    ms = in ? tvalue(vm) : -INFINITY;
-                    ls = in ? tvalue(vl) : 0.f;
-                };
-                // The o values of splits 0..15 are loaded together with block 0's (m, l): one round trip for
-                // contexts up to 2048.
-                auto load_o = [&](int sb, int end, uint64_t (&v)[16]) {
+                const unsigned tag = tg + T_ATT_PART;
+                uint64_t vm = static_cast<uint64_t>(tag) << 32, vl = vm;
+                if (lane < nsplit) {
+                    vm = tload(pp + lane * kPartStride + HD);
+                    vl = tload(pp + lane * kPartStride + HD + 1);
+                }
+                float M = 0.f, e = 0.f, Lsum = 0.f, acc = 0.f;
+#pragma unroll 1
+                for (int sb = 0; sb < nsplit; sb += 16) {
+                    uint64_t v[16];
 #pragma unroll
                     for (int k = 0; k < 16; ++k)
-                        v[k] = sb + k < end ? tload(pp + (sb + k) * kPartStride + lane) : static_cast<uint64_t>(tag) << 32;
-                };
-                auto poll_o = [&](int sb, int end, uint64_t (&v)[16]) {
+                        v[k] = sb + k < nsplit ? tload(pp + (sb + k) * kPartStride + lane) : static_cast<uint64_t>(tag) << 32;
                     unsigned spins = 0;
                     for (;;) {
-                        bool ok = true;
+                        bool ok = tagged(vm, tag) && tagged(vl, tag);
 #pragma unroll
                         for (int k = 0; k < 16; ++k) ok = ok && tagged(v[k], tag);
                         if (ok || give_up(spins, err)) break;
+                        if (!tagged(vm, tag)) vm = tload(pp + lane * kPartStride + HD);
+                        if (!tagged(vl, tag)) vl = tload(pp + lane * kPartStride + HD + 1);
 #pragma unroll
                         for (int k = 0; k < 16; ++k)
-                            if (sb + k < end && !tagged(v[k], tag)) v[k] = tload(pp + (sb + k) * kPartStride + lane);
+                            if (sb + k < nsplit && !tagged(v[k], tag)) v[k] = tload(pp + (sb + k) * kPartStride + lane);
                     }
-                };
-                uint64_t v0[16];
-                load_o(0, min(nsplit, kWave), v0);
-                // Pass 1: the maximum over every split (one block of 64 up to context 8192).
-                float ms0, ls0;
-                poll_ml(0, ms0, ls0);
-                float M = wave_max(ms0);
-#pragma unroll 1
-                for (int sb = kWave; sb < nsplit; sb += kWave) {
-                    float ms, ls;
-                    poll_ml(sb, ms, ls);
-                    M = fmaxf(M, wave_max(ms));
-                }
-                // Pass 2: L and the weighted o, splits in order, 16 o values in flight per round trip.
-                float Lsum = 0.f, acc = 0.f;
-#pragma unroll 1
-                for (int sb64 = 0; sb64 < nsplit; sb64 += kWave) {
-                    float ms = ms0, ls = ls0;
-                    if (sb64 > 0) poll_ml(sb64, ms, ls);
-                    const float e = sb64 + lane < nsplit ? expf(ms - M) : 0.f;
-                    Lsum += wave_sum(ls * e);
-                    const int end = min(nsplit, sb64 + kWave);
-#pragma unroll 1
-                    for (int sb = sb64; sb < end; sb += 16) {
-                        uint64_t v[16];
-                        if (sb == 0) {
-#pragma unroll
-                            for (int k = 0; k < 16; ++k) v[k] = v0[k];
-                        } else {
-                            load_o(sb, end, v);
-                        }
-                        poll_o(sb, end, v);
-#pragma unroll
-                        for (int k = 0; k < 16; ++k)
-                            if (sb + k < end) acc = fmaf(tvalue(v[k]), __shfl(e, sb + k - sb64), acc);
+                    if (sb == 0) {
+                        const float ms = lane < nsplit ? tvalue(vm) : -INFINITY;
+                        const float ls = lane < nsplit ? tvalue(vl) : 0.f;
+                        M = wave_max(ms);
+                        e = lane < nsplit ? expf(ms - M) : 0.f;
+                        Lsum = wave_sum(ls * e);
                     }
+#pragma unroll
+                    for (int k = 0; k < 16; ++k)
+                        if (sb + k < nsplit) acc = fmaf(tvalue(v[k]), __shfl(e, sb + k), acc);
                 }
                 tstore(tatt + h * HD + lane, acc / Lsum, tg + T_ATT);
             }
+        } else if (nsplit > kWave) {
+            merge_long(tpart, tatt, tg, nsplit, NS, gw, NW, lane, err);
         }
         stamp(p, 1 + 6 * l + 2);
 
@@ -1657,23 +1690,42 @@ int decode_max_grid(WType wt) {
     return b * device_cu_count();
 }
 
+namespace {
+
+const void* decode_fn(WType wt) {
+    switch (wt) {
+        case WType::BF16: return reinterpret_cast<const void*>(&dk::decode_kernel<WType::BF16>);
+        case WType::INT8: return reinterpret_cast<const void*>(&dk::decode_kernel<WType::INT8>);
+        case WType::INT4: return reinterpret_cast<const void*>(&dk::decode_kernel<WType::INT4>);
+    }
+    throw ArgError("decode: unknown weight type");
+}
+
+}  // namespace
+
+// A plain launch.  A cooperative launch (hipLaunchCooperativeKernel) would have the runtime guarantee
+// co-residency, but it measured about 18 us per step slower on MI355X for every weight type; the engine
+// instead verifies co-residency once with decode_grid_is_resident, and every wait in the kernel is bounded.
 void launch_decode(WType wt, const DecodeParams& p, int grid, hipStream_t s) {
     CLLM_REQUIRE(grid >= kDecodeMinGrid && grid <= kDecodeMaxGrid && grid % 8 == 0,
                  "decode: grid must be a multiple of 8 in 64..4096 workgroups");
     CLLM_REQUIRE(p.max_seq > 0 && p.max_seq % kAttnChunk == 0 && p.max_seq <= kDecodeMaxSeq,
                  "decode: max_seq must be a multiple of 128 and at most 131072");
-    // A cooperative launch: the runtime either makes every workgroup co-resident or refuses the launch
-    // (hipErrorCooperativeLaunchTooLarge), so the cross-workgroup waits never depend on workgroups that
-    // have not been scheduled.
     DecodeParams arg = p;
     void* args[] = {&arg};
-    const void* fn = nullptr;
-    switch (wt) {
-        case WType::BF16: fn = reinterpret_cast<const void*>(&dk::decode_kernel<WType::BF16>); break;
-        case WType::INT8: fn = reinterpret_cast<const void*>(&dk::decode_kernel<WType::INT8>); break;
-        case WType::INT4: fn = reinterpret_cast<const void*>(&dk::decode_kernel<WType::INT4>); break;
-    }
-    CLLM_HIP(hipLaunchCooperativeKernel(fn, dim3(grid), dim3(kDecodeThreads), args, 0, s));
+    CLLM_HIP(hipLaunchKernel(decode_fn(wt), dim3(grid), dim3(kDecodeThreads), args, 0, s));
+}
+
+bool decode_grid_is_resident(WType wt, const DecodeParams& p, int grid, unsigned* probe, hipStream_t s) {
+    CLLM_REQUIRE(probe, "decode probe: null counter");
+    DecodeParams arg = p;
+    arg.probe = probe;
+    void* args[] = {&arg};
+    CLLM_HIP(hipLaunchKernel(decode_fn(wt), dim3(grid), dim3(kDecodeThreads), args, 0, s));
+    unsigned host[2] = {0, 0};
+    CLLM_HIP(hipMemcpyAsync(host, probe, sizeof(host), hipMemcpyDeviceToHost, s));
+    CLLM_HIP(hipStreamSynchronize(s));
+    return host[1] == 0 && host[0] == static_cast<unsigned>(grid);
 }
 
 }  // namespace cllm

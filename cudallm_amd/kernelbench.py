@@ -83,6 +83,9 @@ def bench_matvec(wd: str, name: str, rows: int, cols: int, ep: str, norm: bool, 
     # Kernel time: events recorded by each dispatch at its kernel's start and end (no launch gap), as a
     # profiler's kernel trace reports it.  Wall time: events between consecutive launches (gaps included).
     kev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(iters)]
+    for a, b in kev:  # torch creates the HIP event at its first record
+        a.record(stream)
+        b.record(stream)
     w0, w1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     w0.record(stream)
     for i in range(iters):
