@@ -407,6 +407,14 @@ int cudallm_launch_attention(const float* q, const unsigned short* k_cache, cons
     });
 }
 
+int cudallm_launch_attention_static(const float* q, const unsigned short* k_cache, const unsigned short* v_cache,
+                                    const int* d_pos, float* out, int nh, int nkv, int hd, int max_seq, void* stream) {
+    return abi_entry("cudallm_launch_attention_static", [&] {
+        cllm::launch_attention_splitk_static(q, k_cache, v_cache, d_pos, out, nh, nkv, hd, max_seq,
+                                             static_cast<hipStream_t>(stream));
+    });
+}
+
 int cudallm_measure_read_bandwidth(unsigned long long bytes, int reps, double* best_gbps, double* median_gbps) {
     return abi_entry("cudallm_measure_read_bandwidth", [&] {
         need(best_gbps && median_gbps, "best_gbps and median_gbps are required");

@@ -55,6 +55,12 @@ void launch_kv_write(const float* qkv, uint16_t* k_cache, uint16_t* v_cache, con
 void launch_attention_splitk(const float* q, const uint16_t* k_cache, const uint16_t* v_cache, const int* d_pos,
                              float* part_o, float* part_ml, float* out, int nh, int nkv, int hd, int max_seq,
                              hipStream_t s);
+// The same split-K attention with its partials in a static device array of kStaticAttnSlots slots
+// (nh * max_seq / 128 <= 8192): no allocation on any call (the array's address on a device is resolved on the first
+// call there).  Calls that overlap on one device share that array and race.
+constexpr int kStaticAttnSlots = 8192;
+void launch_attention_splitk_static(const float* q, const uint16_t* k_cache, const uint16_t* v_cache, const int* d_pos,
+                                    float* out, int nh, int nkv, int hd, int max_seq, hipStream_t s);
 void launch_attention_naive(const float* q, const uint16_t* k_cache, const uint16_t* v_cache, const int* d_pos,
                             float* out, int nh, int nkv, int hd, int max_seq, hipStream_t s);
 

@@ -9,6 +9,9 @@
 // The gfx950 layout is this file's: a 256-thread workgroup = 4 waves = the 4 query heads of one
 // kv head, each lane scores two tokens (lane, lane+64) with the query held in VGPRs, and each lane
 // owns one of the 64 output dimensions for the p.V accumulation.
+#include <array>
+#include <mutex>
+
 #include "../kernels.h"
 #include "device.h"
 
@@ -269,6 +272,47 @@ void launch_attention_naive(const float* q, const uint16_t* k_cache, const uint1
     hipLaunchKernelGGL(attn_naive_kernel, dim3(nh), dim3(256), smem, s, q, k_cache, v_cache, d_pos, out, nh, nkv, hd,
                        max_seq);
     CLLM_HIP(hipGetLastError());
+}
+
+// ---- split-K attention with the partials in static device memory (no allocation on any call) ----------
+
+namespace {
+
+// The split partials of launch_attention_splitk_static: o [slot][64] then (m, l) [slot][2], slot = head * splits +
+// split, for at most kStaticAttnSlots slots.  Each device holds its own copy of this array until the process ends.
+// Its name is a host-side stand-in: host code uses only the address hipGetSymbolAddress reports, per device.
+__device__ __align__(256) float scratch[kStaticAttnSlots * (kHd + 2)];
+
+std::mutex g_scratch_mu;
+std::array<float*, 64> g_scratch{};  // device address of `scratch`, indexed by device (no allocation, host or device)
+
+float* scratch_on_current_device() {
+    int dev = 0;
+    CLLM_HIP(hipGetDevice(&dev));
+    CLLM_REQUIRE(dev >= 0 && dev < static_cast<int>(g_scratch.size()), "attention scratch: device index above 63");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch[dev]) {
+        void* ptr = nullptr;
+        CLLM_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+        CLLM_INTERNAL(ptr, "attention scratch: no device address");
+        g_scratch[dev] = static_cast<float*>(ptr);
+    }
+    return g_scratch[dev];
+}
+
+}  // namespace
+
+void launch_attention_splitk_static(const float* q, const uint16_t* k_cache, const uint16_t* v_cache, const int* d_pos,
+                                    float* out, int nh, int nkv, int hd, int max_seq, hipStream_t s) {
+    CLLM_REQUIRE(nh > 0 && max_seq > 0 && max_seq % kAttnChunk == 0,
+                 "attention (static scratch): max_seq must be a positive multiple of 128");
+    CLLM_REQUIRE(static_cast<long long>(nh) * (max_seq / kAttnChunk) <= kStaticAttnSlots,
+                 "attention (static scratch): nh * max_seq / 128 exceeds the 8192 partial slots of the static scratch");
+    float* base = scratch_on_current_device();
+    // No clearing needed: every split at or before ctx writes its slots before the merge reads them, and the merge
+    // reads no other slot.
+    launch_attention_splitk(q, k_cache, v_cache, d_pos, base, base + static_cast<size_t>(kStaticAttnSlots) * kHd, out,
+                            nh, nkv, hd, max_seq, s);
 }
 
 }  // namespace cllm

@@ -75,6 +75,7 @@ SIGNATURES = {
     "cudallm_launch_matvec_timed": ([c_int, c_int, c_int] + [c_void_p] * 4 + [c_float, c_void_p, c_int, c_int] +
                                     [c_void_p] * 3, c_int),
     "cudallm_launch_attention": ([c_void_p] * 7 + [c_int] * 4 + [c_void_p], c_int),
+    "cudallm_launch_attention_static": ([c_void_p] * 5 + [c_int] * 4 + [c_void_p], c_int),
     "cudallm_measure_read_bandwidth": ([c_ulonglong, c_int, POINTER(c_double), POINTER(c_double)], c_int),
     "cudallm_quantize_int8_rows": ([_F32P, c_int, c_int, POINTER(c_byte), _F32P], c_int),
     "cudallm_quantize_int4_groups": ([_F32P, c_int, c_int, c_int, POINTER(c_ubyte), _U16P], c_int),
@@ -323,6 +324,12 @@ def launch_attention(q_ptr: int, k_ptr: int, v_ptr: int, pos_ptr: int, part_o_pt
     """Split-K attention over ctx = *pos + 1 tokens; part_o / part_ml are the caller's scratch."""
     call("cudallm_launch_attention", q_ptr, k_ptr, v_ptr, pos_ptr, part_o_ptr, part_ml_ptr, out_ptr, nh, nkv, hd,
          max_seq, stream)
+
+
+def launch_attention_static(q_ptr: int, k_ptr: int, v_ptr: int, pos_ptr: int, out_ptr: int, nh: int, nkv: int,
+                            hd: int, max_seq: int, stream: int | None = None) -> None:
+    """launch_attention with its split partials in the library's static device scratch (allocates nothing)."""
+    call("cudallm_launch_attention_static", q_ptr, k_ptr, v_ptr, pos_ptr, out_ptr, nh, nkv, hd, max_seq, stream)
 
 
 def measure_read_bandwidth(nbytes: int = 4 << 30, reps: int = 10) -> tuple[float, float]:

@@ -132,6 +132,14 @@ int cudallm_kernel_argmax(const float* logits, int n, int* out_idx);
 /* Same operands and epilogues as cudallm_kernel_matvec (opt kernel); norm_w != NULL fuses RMSNorm. */
 int cudallm_launch_matvec(int weight_dtype, int epilogue, int rpb, const void* w, const void* scales,
                           const float* x, const float* norm_w, float eps, float* y, int rows, int cols, void* stream);
+/* cudallm_launch_attention without the scratch arguments, for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  No reference counterpart.  The
+ * split partials live in a static device array of 8192 slots (about 2.1 MiB per GPU, held until the process ends),
+ * so nh * max_seq / 128 must be at most 8192 (e.g. 32 heads up to max_seq 32768), else CUDALLM_ERR_INVALID_ARG.
+ * The call allocates nothing.  Calls that overlap on one GPU share that array and race; serialise them (one stream,
+ * or events). */
+int cudallm_launch_attention_static(const float* q, const unsigned short* k_cache, const unsigned short* v_cache,
+                                    const int* d_pos, float* out, int nh, int nkv, int hd, int max_seq, void* stream);
 /* cudallm_launch_matvec whose kernel records start_event / stop_event (hipEvent_t, created by the caller) at its
  * own start and end (hipExtLaunchKernel), so hipEventElapsedTime gives the kernel's duration without the launch
  * gap: what a profiler's kernel trace reports.  For kernel benchmarks. */
