@@ -1,0 +1,147 @@
+"""Summaries of rocprofv3 output for this library's kernels (the tables under profiles/).
+
+    python -m cudallm_amd.profsum trace DIR [--matvec-blocks] [--decode]
+    python -m cudallm_amd.profsum counters FETCH_DIR WRITE_DIR [--calib-bytes N]
+
+``trace``: reads DIR/*kernel_trace.csv (rocprofv3 --kernel-trace).  With --matvec-blocks the matvec dispatches are
+split into contiguous runs of one kernel name (cudallm_amd.kernelbench --op shapes launches qkv, wo, gate_up, down,
+lm_head in that order, and consecutive shapes use different kernel instances), and each run is matched to its shape
+by position; per run: calls, mean / median / min / max duration, and GB/s and the fraction of 8 TB/s from the shape's
+algorithmic bytes.  With --decode: the persistent decode kernels per weight type.
+
+``counters``: two rocprofv3 --pmc runs (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch); each counter is scaled by
+what it reads for the largest __amd_rocclr_copyBuffer dispatch of known size (--calib-bytes, the bench's
+--copy-calib), and the decode kernels' read and write bytes per launch are printed against their algorithmic bytes.
+"""
+import argparse
+import csv
+import glob
+import json
+import statistics
+import sys
+from pathlib import Path
+
+from .kernelbench import SHAPES, matvec_bytes
+
+PEAK = 8.0e12
+WEIGHT_BYTES = {"bf16": 2471764096, "int8": 1238037632, "int4": 637452416}
+DTYPE_OF = {"WType)1": "bf16", "WType)3": "int8", "WType)4": "int4"}
+
+
+def _rows(d: Path, suffix: str):
+    files = sorted(glob.glob(str(d / f"**/*{suffix}"), recursive=True))
+    if not files:
+        raise SystemExit(f"no *{suffix} under {d}")
+    with open(files[0], newline="") as f:
+        return list(csv.DictReader(f))
+
+
+def _dtype(name: str) -> str | None:
+    for k, v in DTYPE_OF.items():
+        if k in name:
+            return v
+    for v in ("bf16", "int8", "int4"):
+        if f"<{v}" in name or f"({v}" in name:
+            return v
+    return None
+
+
+def _stats(us):
+    return {"calls": len(us), "mean_us": statistics.fmean(us), "median_us": statistics.median(us), "min_us": min(us),
+            "max_us": max(us)}
+
+
+def matvec_blocks(rows, wtype: str):
+    disp = [r for r in rows if "matvec" in r["Kernel_Name"]]
+    blocks = []
+    for r in disp:
+        us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+        if blocks and blocks[-1][0] == r["Kernel_Name"]:
+            blocks[-1][1].append(us)
+        else:
+            blocks.append((r["Kernel_Name"], [us]))
+    out = []
+    for (name, us), shape in zip(blocks, SHAPES):
+        sname, rws, cols, ep, norm = shape
+        st = _stats(us)
+        b = matvec_bytes(wtype, rws, cols)
+        st.update(shape=sname, rows=rws, cols=cols, kernel=name.split("(")[0], bytes=b,
+                  gbps=b / st["mean_us"] / 1e3, frac_of_8tbs=b / st["mean_us"] / 1e3 / (PEAK / 1e9))
+        out.append(st)
+    return out
+
+
+PROBE_US = 50.0  # the engine's co-residency probe launch of the decode kernel takes a few microseconds
+
+
+def decode_stats(rows):
+    """Decode steps per weight type; the co-residency probe launches (same kernel, under PROBE_US) are counted
+    apart."""
+    per, probes = {}, {}
+    for r in rows:
+        if "decode_kernel" not in r["Kernel_Name"]:
+            continue
+        wd = _dtype(r["Kernel_Name"])
+        us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+        (probes if us < PROBE_US else per).setdefault(wd, []).append(us)
+    out = {wd: _stats(us) for wd, us in per.items()}
+    for wd, us in probes.items():
+        out.setdefault(wd, {})["probe_launches"] = len(us)
+    return out
+
+
+def counters(fetch_dir: Path, write_dir: Path, calib_bytes: int):
+    def load(d, counter):
+        rows = [r for r in _rows(d, "counter_collection.csv") if r["Counter_Name"] == counter]
+        copies = [float(r["Counter_Value"]) for r in rows if r["Kernel_Name"] == "__amd_rocclr_copyBuffer"]
+        dec = {}
+        for r in rows:
+            if "decode_kernel" in r["Kernel_Name"]:
+                dec.setdefault(_dtype(r["Kernel_Name"]), []).append(float(r["Counter_Value"]))
+        return (max(copies) if copies else None), dec
+    fc, fd = load(fetch_dir, "FETCH_SIZE")
+    wc, wdc = load(write_dir, "WRITE_SIZE")
+    ffac = calib_bytes / (fc * 1024) if fc else None
+    wfac = calib_bytes / (wc * 1024) if wc else None
+    out = {"copy_calibration": {"bytes": calib_bytes, "fetch_kib": fc, "write_kib": wc, "fetch_factor": ffac,
+                                "write_factor": wfac}, "kernels": {}}
+    for wd in sorted(set(fd) | set(wdc)):
+        f = statistics.median(fd.get(wd, [0])) if fd.get(wd) else None
+        w = statistics.median(wdc.get(wd, [0])) if wdc.get(wd) else None
+        e = {"dispatches": len(fd.get(wd, [])), "fetch_kib": f, "write_kib": w}
+        if f is not None and ffac:
+            e["read_bytes"] = f * 1024 * ffac
+            e["read_over_weight_bytes"] = e["read_bytes"] / WEIGHT_BYTES[wd]
+        if w is not None and wfac:
+            e["write_bytes"] = w * 1024 * wfac
+        out["kernels"][f"decode_kernel<{wd}>"] = e
+    return out
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description="summaries of rocprofv3 output")
+    sub = ap.add_subparsers(dest="cmd", required=True)
+    t = sub.add_parser("trace")
+    t.add_argument("dir", type=Path)
+    t.add_argument("--matvec-blocks", metavar="WTYPE")
+    t.add_argument("--decode", action="store_true")
+    c = sub.add_parser("counters")
+    c.add_argument("fetch_dir", type=Path)
+    c.add_argument("write_dir", type=Path)
+    c.add_argument("--calib-bytes", type=int, default=1 << 30)
+    args = ap.parse_args(argv)
+    if args.cmd == "trace":
+        rows = _rows(args.dir, "kernel_trace.csv")
+        res = {}
+        if args.matvec_blocks:
+            res["matvec"] = matvec_blocks(rows, args.matvec_blocks)
+        if args.decode:
+            res["decode"] = decode_stats(rows)
+    else:
+        res = counters(args.fetch_dir, args.write_dir, args.calib_bytes)
+    print(json.dumps(res, indent=1))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
