@@ -51,7 +51,21 @@ constexpr unsigned kSpinCap = 1u << 20;     // bounded waits on other workgroups
 constexpr unsigned kLdsSpinCap = 1u << 26;  // bounded waits inside the workgroup (a few seconds)
 constexpr int kPartStride = HD + 2;      // o[64], m, l
 constexpr int kPairs = QKV / 2;          // RoPE pairs (i, i+32) of every q/k/v head
-constexpr int kLmR = 2;                  // lm_head rows per unit
+// Tuning knobs of the decode kernel, overridable at build time (cudallm_amd/sweep_decode.py sweeps them): lines in
+// flight per loader wave, ring slots per compute wave (bf16 / quantised), lm_head rows per unit.
+#ifndef CLLM_LOADER_LINES
+#define CLLM_LOADER_LINES 16
+#endif
+#ifndef CLLM_RING_SLOTS_BF16
+#define CLLM_RING_SLOTS_BF16 30
+#endif
+#ifndef CLLM_RING_SLOTS_QUANT
+#define CLLM_RING_SLOTS_QUANT 20
+#endif
+#ifndef CLLM_LM_ROWS
+#define CLLM_LM_ROWS 2
+#endif
+constexpr int kLmR = CLLM_LM_ROWS;       // lm_head rows per unit
 static_assert(VOCAB % kLmR == 0, "lm_head units");
 
 enum : unsigned { T_QKV = 0, T_ATT_PART = 1, T_ATT = 2, T_XA = 3, T_ACT = 4, T_X = 5 };
@@ -86,13 +100,13 @@ static_assert(kDecodeMinGrid * kCW * kRPW >= H, "residual rows per wave");
 template <WType WT>
 struct RingCfg {
     static constexpr bool kQuant = WT != WType::BF16;
-    static constexpr int S = kQuant ? 20 : 30;                 // 1 KiB slots per compute wave (bf16: what fits)
+    static constexpr int S = kQuant ? CLLM_RING_SLOTS_QUANT : CLLM_RING_SLOTS_BF16;  // 1 KiB slots per compute wave
     static constexpr int SS = kQuant ? S : 1;                  // side-value slots
     static constexpr int LPR2 = Fmt<WT>::CPL;                  // lines per 2048-wide row
     static constexpr int LPR8 = INTER / Fmt<WT>::CPC / kWave;  // lines per 8192-wide row
-    // Lines in flight per loader wave (16, measured on MI355X against 12: deeper queues also delay the
-    // small polling loads of the phase handoffs behind them; 12 and 16 are within a few us).
-    static constexpr int NB = 16;
+    // Lines in flight per loader wave (16 measured best on MI355X: deeper queues also delay the small polling loads of
+    // the phase handoffs behind them).
+    static constexpr int NB = CLLM_LOADER_LINES;
 };
 
 template <WType WT>
