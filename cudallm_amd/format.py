@@ -1,8 +1,9 @@
 """Reader/writer for the ``.cudallm`` weight-file format.
 
-Same format and function names as the reference's ``python/cudallm/format.py:7-147``
-(``src/model/cudallm_format.h:12-41``): a 256-byte header, 80-byte tensor entries, 256-byte
-aligned tensor data with zero padding only before each tensor.
+The format is the reference's (``src/model/cudallm_format.h:12-41``, ``python/cudallm/format.py:7-147``): a 256-byte
+header, 80-byte tensor entries, 256-byte aligned tensor data with zero padding only before each tensor; the constants
+below are that format.  The function names are those the reference's Python tools call; the parsing is numpy
+record types, and the writer streams one tensor at a time.
 """
 import struct
 from pathlib import Path
@@ -32,30 +33,31 @@ def _align(n: int) -> int:
     return (n + ALIGN - 1) // ALIGN * ALIGN
 
 
+# Storage of each tensor dtype code: (numpy dtype of one stored element, logical columns per stored element).
+_STORAGE = {F32: (np.dtype("<f4"), 1), BF16: (np.dtype("<u2"), 1), F16: (np.dtype("<f2"), 1), I8: (np.dtype("i1"), 1),
+            I4X2: (np.dtype("u1"), 2)}
+
+
 def expected_nbytes(dtype: int, rows: int, cols: int) -> int:
-    if dtype == F32:
-        return rows * cols * 4
-    if dtype in (BF16, F16):
-        return rows * cols * 2
-    if dtype == I8:
-        return rows * cols
-    if dtype == I4X2:
-        if cols % 2:
-            raise ValueError("I4X2 needs an even column count")
-        return rows * cols // 2
-    raise ValueError(f"unknown dtype code {dtype}")
+    """Bytes of a rows x cols tensor of `dtype` (I4X2 packs two columns per byte, so cols must be even)."""
+    if dtype not in _STORAGE:
+        raise ValueError(f"tensor dtype code {dtype} is not one of F32, BF16, F16, I8, I4X2")
+    np_dt, per = _STORAGE[dtype]
+    if cols % per:
+        raise ValueError(f"dtype code {dtype} stores {per} columns per byte; {cols} columns do not divide")
+    return rows * (cols // per) * np_dt.itemsize
 
 
 def expected_names(n_layers: int, quant: bool) -> list[str]:
-    names = ["rope.inv_freq", "tok_embeddings.weight"] + (["tok_embeddings.scales"] if quant else []) + ["norm.weight"]
+    """The fixed tensor sequence (src/model/weights.cpp:66-81): every linear is `.weight`, plus `.scales` when the
+    file is quantised."""
+    def linear(name):
+        return [name + ".weight", name + ".scales"] if quant else [name + ".weight"]
+    names = ["rope.inv_freq", *linear("tok_embeddings"), "norm.weight"]
     for i in range(n_layers):
         p = f"layers.{i}."
-        names.append(p + "attn_norm.weight")
-        for lin in ("wqkv", "wo"):
-            names += [p + lin + ".weight"] + ([p + lin + ".scales"] if quant else [])
-        names.append(p + "ffn_norm.weight")
-        for lin in ("w_gate_up", "w_down"):
-            names += [p + lin + ".weight"] + ([p + lin + ".scales"] if quant else [])
+        names += [p + "attn_norm.weight", *linear(p + "wqkv"), *linear(p + "wo"), p + "ffn_norm.weight",
+                  *linear(p + "w_gate_up"), *linear(p + "w_down")]
     return names
 
 
@@ -110,39 +112,57 @@ def write_cudallm(path, header: dict, tensors: list[tuple[str, int, int, int, by
     w.close()
 
 
+# The header and table entries as numpy record types (little-endian, packed), the same layout as HEADER_FMT /
+# ENTRY_FMT: one np.frombuffer / np.fromfile call parses them.
+_HEADER_DT = np.dtype([("magic", "S4"), ("version", "<u4"), ("weight_dtype", "<u4"), ("hidden_size", "<u4"),
+                       ("intermediate_size", "<u4"), ("n_layers", "<u4"), ("n_heads", "<u4"), ("n_kv_heads", "<u4"),
+                       ("head_dim", "<u4"), ("vocab_size", "<u4"), ("max_seq_len", "<u4"), ("rms_eps", "<f4"),
+                       ("rope_theta", "<f4"), ("group_size", "<u4"), ("n_tensors", "<u4"), ("reserved0", "<u4"),
+                       ("table_offset", "<u8")])
+_ENTRY_DT = np.dtype([("name", "S48"), ("dtype", "<u4"), ("rows", "<u4"), ("cols", "<u4"), ("reserved", "<u4"),
+                      ("offset", "<u8"), ("nbytes", "<u8")])
+assert _HEADER_DT.itemsize == struct.calcsize(HEADER_FMT) and _ENTRY_DT.itemsize == ENTRY_SIZE
+
+
+def _python(v):
+    return v.item() if hasattr(v, "item") else v
+
+
 def read_header(path) -> dict:
+    """The header's fields by name (HEADER_FIELDS), as Python numbers (magic stays bytes)."""
     with open(path, "rb") as f:
         raw = f.read(HEADER_SIZE)
-    if len(raw) != HEADER_SIZE:
-        raise ValueError(f"{path}: truncated header")
-    return dict(zip(HEADER_FIELDS, struct.unpack(HEADER_FMT, raw[:struct.calcsize(HEADER_FMT)])))
+    if len(raw) < HEADER_SIZE:
+        raise ValueError(f"{path}: file ends inside the {HEADER_SIZE}-byte header ({len(raw)} bytes)")
+    rec = np.frombuffer(raw, dtype=_HEADER_DT, count=1)[0]
+    return {name: _python(rec[name]) for name in HEADER_FIELDS}
 
 
 def read_table(path) -> list[dict]:
+    """The tensor entries in file order, each a dict with name, dtype, rows, cols, reserved, offset, nbytes."""
     hdr = read_header(path)
-    with open(path, "rb") as f:
-        f.seek(hdr["table_offset"])
-        raw = f.read(ENTRY_SIZE * hdr["n_tensors"])
-    out = []
-    for k in range(hdr["n_tensors"]):
-        name, dtype, rows, cols, reserved, offset, nbytes = struct.unpack_from(ENTRY_FMT, raw, k * ENTRY_SIZE)
-        out.append({"name": name.rstrip(b"\0").decode("ascii"), "dtype": dtype, "rows": rows, "cols": cols,
-                    "reserved": reserved, "offset": offset, "nbytes": nbytes})
-    return out
+    n = hdr["n_tensors"]
+    recs = np.fromfile(path, dtype=_ENTRY_DT, count=n, offset=hdr["table_offset"])
+    if len(recs) != n:
+        raise ValueError(f"{path}: the table should hold {n} entries but the file ends after {len(recs)}")
+    table = []
+    for rec in recs:
+        e = {f: _python(rec[f]) for f in _ENTRY_DT.names}
+        e["name"] = rec["name"].split(b"\0", 1)[0].decode("ascii")
+        table.append(e)
+    return table
 
 
 def load_tensor(path, entry: dict) -> np.ndarray:
-    rows, cols, dtype = entry["rows"], entry["cols"], entry["dtype"]
-    np_dtype, shape = {F32: (np.float32, (rows, cols)), BF16: (np.uint16, (rows, cols)),
-                       F16: (np.float16, (rows, cols)), I8: (np.int8, (rows, cols)),
-                       I4X2: (np.uint8, (rows, cols // 2))}[dtype]
-    count = shape[0] * shape[1]
-    arr = np.fromfile(path, dtype=np_dtype, count=count, offset=entry["offset"])
-    if arr.size != count:
-        raise ValueError(f"{path}: truncated tensor {entry['name']}")
-    arr = arr.reshape(shape)
-    return arr.reshape(rows) if dtype == F32 and cols == 1 else arr
-
-
-def bf16_bits_to_f32(bits: np.ndarray) -> np.ndarray:
-    return (bits.astype(np.uint32) << 16).view(np.float32)
+    """One tensor as stored: F32 [rows, cols] (a vector when cols == 1), BF16 as uint16 bits, F16, I8, and I4X2
+    as uint8 [rows, cols / 2]."""
+    np_dt, per = _STORAGE[entry["dtype"]]
+    rows, cols = entry["rows"], entry["cols"]
+    out = np.empty((rows, cols // per), dtype=np_dt)
+    with open(path, "rb") as f:
+        f.seek(entry["offset"])
+        got = f.readinto(memoryview(out).cast("B"))
+    if got != out.nbytes:
+        raise ValueError(f"{path}: {entry['name']} needs {out.nbytes} bytes at offset {entry['offset']}, "
+                         f"the file holds {got}")
+    return out.reshape(rows) if entry["dtype"] == F32 and cols == 1 else out

@@ -57,15 +57,16 @@ def tokenizer(tokenizer_dir):
 # ---- eval_ppl -------------------------------------------------------------------------------------------------
 
 def test_nll_from_logits():
-    """Against scipy's logsumexp in float64, with an fp32 offset that would overflow a naive exp; uniform logits
-    give log(n) exactly."""
-    from scipy.special import logsumexp
-    rng = np.random.default_rng(0)
-    z = (rng.standard_normal(5000) * 4 + 1e4).astype(np.float32)
-    for t in (0, 17, 4999):
-        want = logsumexp(z.astype(np.float64)) - float(z[t])
-        assert math.isclose(P.nll_from_logits(z, t), want, rel_tol=1e-12, abs_tol=1e-9)
+    """Closed forms: logits (0, ln 3) are probabilities (1/4, 3/4); uniform logits give log(n); a common offset that
+    would overflow a naive exp does not change the result; and the token NLLs of a random row sum, after exp, to
+    softmax's total of 1."""
+    z = np.array([0.0, math.log(3.0)], np.float32)
+    assert math.isclose(P.nll_from_logits(z, 0), math.log(4.0), rel_tol=1e-6)
+    assert math.isclose(P.nll_from_logits(z, 1), math.log(4.0 / 3.0), rel_tol=1e-6)
+    assert math.isclose(P.nll_from_logits(z + np.float32(1e4), 0), math.log(4.0), rel_tol=1e-6)
     assert math.isclose(P.nll_from_logits(np.zeros(VOCAB, np.float32), 5), math.log(VOCAB), rel_tol=1e-14)
+    r = (np.random.default_rng(0).standard_normal(5000) * 4).astype(np.float32)
+    assert math.isclose(sum(math.exp(-P.nll_from_logits(r, t)) for t in range(r.size)), 1.0, rel_tol=1e-9)
 
 
 def test_windows_and_perplexity():
