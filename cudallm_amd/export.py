@@ -158,10 +158,10 @@ def export(hf_dir, out, dtype: str, check: bool = True) -> int:
 
     ck = _Checkpoint(hf_dir)
     if "lm_head.weight" in ck.keys():
-        raise ValueError("unexpected lm_head.weight (embeddings must be tied)")
+        raise ValueError("the checkpoint has its own lm_head.weight; this format stores one embedding for both ends")
     missing = [k for k in expected_hf_keys(n_layers) if k not in ck.keys()]
     if missing:
-        raise ValueError(f"missing HF tensors: {missing[:5]}")
+        raise ValueError(f"{len(missing)} tensors the format needs are absent from the checkpoint, e.g. {missing[:5]}")
 
     qkv_rows = (nh + 2 * nkv) * hd
     specs = [("rope.inv_freq", fmt.F32, inv_freq.size, 1)]
@@ -176,7 +176,7 @@ def export(hf_dir, out, dtype: str, check: bool = True) -> int:
         specs += _linear_specs(p + "w_gate_up", 2 * I, H, dtype)
         specs += _linear_specs(p + "w_down", H, I, dtype)
     if [s[0] for s in specs] != fmt.expected_names(n_layers, dtype != "bf16"):
-        raise AssertionError("tensor order does not match the .cudallm format")
+        raise AssertionError("internal: the tensors were produced in another order than the file's table")
 
     header = {"weight_dtype": {"bf16": fmt.WEIGHT_BF16, "int8": fmt.WEIGHT_INT8, "int4": fmt.WEIGHT_INT4}[dtype],
               "hidden_size": H, "intermediate_size": I, "n_layers": n_layers, "n_heads": nh, "n_kv_heads": nkv,
