@@ -11,7 +11,8 @@
 //    loop reads no LDS at all: only 128-bit non-temporal weight loads, 64 lanes x 16 B = 1 KiB
 //    contiguous per load instruction.
 //  * R rows (rpb) are loaded before any is consumed, for R x (4 KiB bf16 | 2 KiB int8 | 1 KiB int4)
-//    of loads in flight per wave.
+//    of loads per pass; a wave issues the next pass's loads before it multiplies the current one,
+//    so up to 2R rows are in flight.
 //  * Row sums are wave64 DPP butterflies (deterministic order); with KS > 1 the slice partials
 //    meet in LDS and are added in slice order.  No atomics anywhere.
 //  * The grid is persistent: min(row blocks, CUs x resident workgroups per CU).
@@ -94,46 +95,55 @@ __global__ void __launch_bounds__(kThreads) matvec_fast(MatvecArgs a) {
     const size_t rb = row_bytes<WT>(a.cols);
     const char* wl = static_cast<const char*>(a.w) + static_cast<size_t>(slice) * (kSlice * 16 / F::CPC) + lane * 16;
     const int groups_per_row = a.cols / 128;
+    // int4: one 128-column group per lane; lanes 4g..4g+3 share scale g of the slice.
+    const uint16_t* gsc = static_cast<const uint16_t*>(a.scales) + slice * (kSlice / 128) + lane / 4;
 
-    for (int base = blockIdx.x * ROWS_WG; base < out_rows; base += gridDim.x * ROWS_WG) {
-        const int r0 = base + grp * R;
+    // The R rows of one pass: weight chunks and, for int4, the lane's group scales.  Two of these alternate, so the
+    // next pass's loads are in flight while this pass is multiplied.
+    struct Block {
         u32x4 v[R][F::CPL];
         u32x4 vu[GLU ? R : 1][F::CPL];
+        uint16_t g[R], gu[R];
+    };
+    auto load = [&](Block& b, int r0) {
 #pragma unroll
         for (int i = 0; i < R; ++i) {
             const int r = r0 + i;
 #pragma unroll
             for (int k = 0; k < F::CPL; ++k) {
                 if (r < out_rows) {
-                    v[i][k] = load_stream(wl + static_cast<size_t>(r) * rb + k * 1024);
-                    if constexpr (GLU) vu[i][k] = load_stream(wl + static_cast<size_t>(r + out_rows) * rb + k * 1024);
+                    b.v[i][k] = load_stream(wl + static_cast<size_t>(r) * rb + k * 1024);
+                    if constexpr (GLU) b.vu[i][k] = load_stream(wl + static_cast<size_t>(r + out_rows) * rb + k * 1024);
                 } else {
-                    v[i][k] = u32x4{0, 0, 0, 0};
-                    if constexpr (GLU) vu[i][k] = u32x4{0, 0, 0, 0};
+                    b.v[i][k] = u32x4{0, 0, 0, 0};
+                    if constexpr (GLU) b.vu[i][k] = u32x4{0, 0, 0, 0};
                 }
             }
+            if constexpr (WT == WType::INT4) {
+                const int rc = min(r, out_rows - 1);
+                b.g[i] = gsc[static_cast<size_t>(rc) * groups_per_row];
+                if constexpr (GLU) b.gu[i] = gsc[static_cast<size_t>(rc + out_rows) * groups_per_row];
+            }
         }
+    };
+    auto pass = [&](const Block& b, int base) {
+        const int r0 = base + grp * R;
         float d[R], du[R];
 #pragma unroll
         for (int i = 0; i < R; ++i) {
             float s = 0.f, su = 0.f;
 #pragma unroll
             for (int k = 0; k < F::CPL; ++k) {
-                s += chunk_dot<WT>(v[i][k], xr + k * F::CPC);
-                if constexpr (GLU) su += chunk_dot<WT>(vu[i][k], xr + k * F::CPC);
+                s += chunk_dot<WT>(b.v[i][k], xr + k * F::CPC);
+                if constexpr (GLU) su += chunk_dot<WT>(b.vu[i][k], xr + k * F::CPC);
             }
             if constexpr (WT == WType::INT8) {
                 s -= kBias<WT> * xsum;
                 if constexpr (GLU) su -= kBias<WT> * xsum;
             }
             if constexpr (WT == WType::INT4) {
-                // One 128-column group per lane: lanes 4g..4g+3 share scale g of the slice.
-                const int r = min(r0 + i, out_rows - 1);
-                const uint16_t* sc = static_cast<const uint16_t*>(a.scales);
-                const int gi = slice * (kSlice / 128) + lane / 4;
-                s = half_bits_to_float(sc[static_cast<size_t>(r) * groups_per_row + gi]) * (s - 8.f * xsum);
-                if constexpr (GLU)
-                    su = half_bits_to_float(sc[static_cast<size_t>(r + out_rows) * groups_per_row + gi]) * (su - 8.f * xsum);
+                s = half_bits_to_float(b.g[i]) * (s - 8.f * xsum);
+                if constexpr (GLU) su = half_bits_to_float(b.gu[i]) * (su - 8.f * xsum);
             }
             d[i] = wave_sum(s);
             du[i] = GLU ? wave_sum(su) : 0.f;
@@ -182,6 +192,23 @@ __global__ void __launch_bounds__(kThreads) matvec_fast(MatvecArgs a) {
             }
             __syncthreads();
         }
+    };
+
+    // base is the same for every wave of the workgroup, so the __syncthreads in pass() is reached by all of them.
+    const int stride = gridDim.x * ROWS_WG;
+    int base = blockIdx.x * ROWS_WG;
+    if (base >= out_rows) return;
+    Block A, B;
+    load(A, base + grp * R);
+    for (;;) {
+        if (base + stride < out_rows) load(B, base + stride + grp * R);
+        pass(A, base);
+        base += stride;
+        if (base >= out_rows) break;
+        if (base + stride < out_rows) load(A, base + stride + grp * R);
+        pass(B, base);
+        base += stride;
+        if (base >= out_rows) break;
     }
 }
 
