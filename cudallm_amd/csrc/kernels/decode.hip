@@ -465,7 +465,13 @@ __device__ __forceinline__ int swz(int i) {
 // With MX = 1, each wave also leaves max |x_i g_i| over the entries it copied in pmax[wave] (g: the
 // norm weights, read while the wait runs), from which the fixed-point scale of the integer dot
 // products is derived; with MX = 2, max |x_i|.
-template <int N, bool SQ, int SWZ = 0, int MX = 0>
+//
+// With TWO, each thread first polls only its last entry and loads the others once that one is current: a wait
+// that starts long before the producers finish then keeps 1/PT of the polls in flight, which leaves the memory
+// path to the producers' stores.  Measured on MI355X for the wo input, which every workgroup starts polling while
+// the few attention workgroups still compute: int4 -16, int8 -4 us per step (bf16 +3, so bf16 keeps one stage),
+// and for int8's gate_up input a further -9 us.
+template <int N, bool SQ, int SWZ = 0, int MX = 0, bool TWO = false>
 __device__ __forceinline__ void fetch(const uint64_t* src, unsigned tag, float* dst, float* part, unsigned* err, int tid,
                       const float* g = nullptr, float* pmax = nullptr) {
     constexpr int PT = N / kCT;
@@ -476,6 +482,10 @@ __device__ __forceinline__ void fetch(const uint64_t* src, unsigned tag, float* 
     if constexpr (MXG)
 #pragma unroll
         for (int k = 0; k < PT; ++k) gv[k] = gload(g + tid + k * kCT);
+    if constexpr (TWO) {
+        uint64_t f = tload(src + tid + (PT - 1) * kCT);
+        while (!tagged(f, tag) && !give_up(spins, err)) f = tload(src + tid + (PT - 1) * kCT);
+    }
     uint64_t v[PT];
 #pragma unroll
     for (int k = 0; k < PT; ++k) v[k] = tload(src + tid + k * kCT);
@@ -548,6 +558,29 @@ __device__ __forceinline__ int dig_exponent(float m) {
     return 21 - ilogbf(m);
 }
 
+// Byte planes of four 24-bit words: P[j] byte i = byte j of a_i (v_perm_b32 picks bytes of {s0, s1}; selector
+// 0-3 = s1's bytes, 4-7 = s0's, 12 = zero).  Seven permutes instead of a shift, mask and insert per byte.
+__device__ __forceinline__ void byte_planes(uint32_t a0, uint32_t a1, uint32_t a2, uint32_t a3, uint32_t (&P)[3]) {
+    const uint32_t t01 = __builtin_amdgcn_perm(a1, a0, 0x05010400u), t23 = __builtin_amdgcn_perm(a3, a2, 0x05010400u);
+    P[0] = __builtin_amdgcn_perm(t23, t01, 0x05040100u);
+    P[1] = __builtin_amdgcn_perm(t23, t01, 0x07060302u);
+    const uint32_t s01 = __builtin_amdgcn_perm(a1, a0, 0x0c0c0602u), s23 = __builtin_amdgcn_perm(a3, a2, 0x0c0c0602u);
+    P[2] = __builtin_amdgcn_perm(s23, s01, 0x05040100u);
+}
+
+// The six base-16 digit words of eight 24-bit offset values u[b] (column b at nibble b): byte planes of the
+// even and the odd columns, whose low and high nibbles interleave into digits 2j and 2j + 1.
+__device__ __forceinline__ void nibble_words(const uint32_t (&u)[8], uint32_t (&w)[6]) {
+    uint32_t E[3], O[3];
+    byte_planes(u[0], u[2], u[4], u[6], E);
+    byte_planes(u[1], u[3], u[5], u[7], O);
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+        w[2 * j] = ((O[j] << 4) & 0xF0F0F0F0u) | (E[j] & 0x0F0F0F0Fu);
+        w[2 * j + 1] = (O[j] & 0xF0F0F0F0u) | ((E[j] >> 4) & 0x0F0F0F0Fu);
+    }
+}
+
 // The norm weights of columns 8 tid .. 8 tid + 7, loaded before the phase waits for its input so that the
 // digit prologue after the wait does not start a memory round trip of its own.
 struct Norm8 {
@@ -572,23 +605,18 @@ __device__ void make_digits(const float* x, const Norm8& gn, float inv, int e, u
         u[c] = (static_cast<uint32_t>(xi) + D::C) ^ D::C;
     }
     if constexpr (WT == WType::INT8) {
+        uint32_t P[2][3];
+        byte_planes(u[0], u[1], u[2], u[3], P[0]);
+        byte_planes(u[4], u[5], u[6], u[7], P[1]);
 #pragma unroll
         for (int k = 0; k < 3; ++k)
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                uint32_t w = 0;
-#pragma unroll
-                for (int b = 0; b < 4; ++b) w |= ((u[4 * h + b] >> (8 * k)) & 0xffu) << (8 * b);
-                tab[k * D::WPD + 2 * tid + h] = w;
-            }
+            for (int h = 0; h < 2; ++h) tab[k * D::WPD + 2 * tid + h] = P[h][k];
     } else {
+        uint32_t w[6];
+        nibble_words(u, w);
 #pragma unroll
-        for (int k = 0; k < 6; ++k) {
-            uint32_t w = 0;
-#pragma unroll
-            for (int b = 0; b < 8; ++b) w |= ((u[b] >> (4 * k)) & 0xfu) << (4 * b);
-            tab[k * D::WPD + tid] = w;
-        }
+        for (int k = 0; k < 6; ++k) tab[k * D::WPD + tid] = w[k];
     }
 }
 
@@ -764,13 +792,7 @@ __device__ __forceinline__ void down_digits(const float* a, int e, int tid, uint
             const float xc = c < 4 ? x0[c] : x1[c - 4];
             u[c] = (static_cast<uint32_t>(static_cast<int>(rintf(ldexpf(xc, e)))) + C) ^ C;
         }
-#pragma unroll
-        for (int k = 0; k < 6; ++k) {
-            uint32_t w = 0;
-#pragma unroll
-            for (int b = 0; b < 8; ++b) w |= ((u[b] >> (4 * k)) & 0xfu) << (4 * b);
-            dw[j][k] = w;
-        }
+        nibble_words(u, dw[j]);
     }
 }
 
@@ -824,15 +846,13 @@ __device__ __forceinline__ void down_digits8(const float* a, int e, int tid, uin
             const float xc = c < 4 ? x0[c] : x1[c - 4];
             u[c] = (static_cast<uint32_t>(static_cast<int>(rintf(ldexpf(xc, e)))) + C) ^ C;
         }
+        uint32_t P[2][3];
+        byte_planes(u[0], u[1], u[2], u[3], P[0]);
+        byte_planes(u[4], u[5], u[6], u[7], P[1]);
 #pragma unroll
         for (int k = 0; k < 3; ++k)
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                uint32_t w = 0;
-#pragma unroll
-                for (int b = 0; b < 4; ++b) w |= ((u[4 * h + b] >> (8 * k)) & 0xffu) << (8 * b);
-                dw[j][2 * k + h] = w;
-            }
+            for (int h = 0; h < 2; ++h) dw[j][2 * k + h] = P[h][k];
     }
 }
 
@@ -1418,7 +1438,7 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
         {
             stall_at(p, kStallWo);
             if constexpr (!kDig) cwait(sm.bar, ep_in, lbad);  // every wave has read the qkv input (as above)
-            fetch<H, false>(tatt, tg + T_ATT, sm.big, sm.part, err, tid);
+            fetch<H, false, 0, 0, kDig>(tatt, tg + T_ATT, sm.big, sm.part, err, tid);
             cbar(sm.bar, ep, wave, lane, lbad);
             stamp_in(p, l, 3, 0);
             stall_at(p, kStallInputs);
@@ -1453,7 +1473,7 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
             stall_at(p, kStallGateUp);
             if constexpr (kDig) {
                 const Norm8 gn = load_norm8(Lw.ffn_norm, tid);
-                fetch<H, true, 0, true>(txa, tg + T_XA, sm.big + kXgu<WT>, sm.part, err, tid, Lw.ffn_norm, sm.pmax);
+                fetch<H, true, 0, 1, WT == WType::INT8>(txa, tg + T_XA, sm.big + kXgu<WT>, sm.part, err, tid, Lw.ffn_norm, sm.pmax);
                 cbar(sm.bar, ep, wave, lane, lbad);
                 stamp_in(p, l, 4, 0);
                 stall_at(p, kStallInputs);
@@ -1541,6 +1561,7 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
                 stall_at(p, kStallInputs);
                 down_sums<WT>(sm.big, lane, dsum);
             }
+            stamp_in(p, l, 5, 1);
             drain();
             int k = wave * kRPW;
 #pragma unroll 1

@@ -6,8 +6,9 @@ Writes a seeded synthetic Llama-3.2-1B-shaped file per weight type, decodes to c
 `reps` profiled steps and keeps the last one.  Each workgroup stamps the GPU's 100 MHz clock when it
 finishes each phase; a phase's time is the median (over workgroups) end of that phase minus the median
 end of the phase before it, so a phase's figure includes the wait for its input.  For layer 1 the table
-also splits each phase into "input arrived" (the handoff) and the rest, and gives the spread of phase
-ends over workgroups (the skew the next handoff waits for).
+also splits each phase into "input arrived" (the handoff), "prologue done" (the input is in registers or in
+the digit table) and the rows, and gives the spread of phase ends over workgroups (the skew the next handoff
+waits for).
 """
 import argparse
 import sys
@@ -58,18 +59,23 @@ def summarise(wd: str, S: np.ndarray, ctx: int) -> list[str]:
     lines.append(f"| **step** | **{argmax_end:.1f}** | |")
     lines += ["", "Layer 1, per phase (us after the previous phase's median end): input arrived (median over "
                   "workgroups that stamp it), phase end median, and the spread of phase ends (p10 / max - median).", "",
-              "| phase | input arrived | end (median) | end p10 | end max |", "|---|---|---|---|---|"]
+              "| phase | input arrived | prologue done | end (median) | end p10 | end max |", "|---|---|---|---|---|---|"]
     pe = np.median(rel[:, 6])  # layer 0 down end
     for k, p in enumerate(PHASES):
         e = rel[:, 7 + k]
         med = np.median(e)
-        inp = ""
+        inp = pro = ""
         if k in (0, 1, 3, 4, 5):
             a = rel[:, 100 + 2 * k]
             a = a[S[:, 100 + 2 * k] > 0]
             if a.size:
                 inp = f"+{np.median(a) - pe:.2f}"
-        lines.append(f"| {p} | {inp} | +{med - pe:.2f} | {np.percentile(e, 10) - med:+.2f} | {e.max() - med:+.2f} |")
+            b = rel[:, 101 + 2 * k]
+            b = b[S[:, 101 + 2 * k] > 0]
+            if b.size:
+                pro = f"+{np.median(b) - pe:.2f}"
+        lines.append(f"| {p} | {inp} | {pro} | +{med - pe:.2f} | {np.percentile(e, 10) - med:+.2f} | "
+                     f"{e.max() - med:+.2f} |")
         pe = med
     return lines + [""]
 
@@ -80,6 +86,7 @@ def main(argv=None) -> int:
     ap.add_argument("--ctx", type=int, default=40)
     ap.add_argument("--reps", type=int, default=5)
     ap.add_argument("--out", type=Path)
+    ap.add_argument("--raw", type=Path, help="also save each weight type's stamps as RAW/stamps_<dtype>.npy")
     args = ap.parse_args(argv)
     from . import synth
     out = []
@@ -88,6 +95,9 @@ def main(argv=None) -> int:
             path = Path(d) / f"profile_{wd}.cudallm"
             synth.write_model(path, wd, seed=1234)
             S = profile(path, args.ctx, args.reps)
+            if args.raw:
+                args.raw.mkdir(parents=True, exist_ok=True)
+                np.save(args.raw / f"stamps_{wd}.npy", S)
             block = summarise(wd, S, args.ctx)
             print("\n".join(block), flush=True)
             out += block
