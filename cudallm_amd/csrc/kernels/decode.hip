@@ -291,11 +291,15 @@ struct Stream {
     int gw, NW;
     int l = 0, seg = 0;
     bool have = false, end = false;
-    int lpr = 1, rpu = 1;   // lines per row, rows per unit
-    int lc = 0, rl = 0, ul = 0;  // lines left in the row, rows left in the unit, units left
-    const char *cur = nullptr, *rowp = nullptr, *unitp = nullptr;     // weight line / row / unit
-    const char *scur = nullptr, *srowp = nullptr, *sunitp = nullptr;  // their side values
-    size_t kstr = 0, ustr = 0, skstr = 0, sustr = 0, sline = 0;
+    int lpr = 1, rpu = 1;        // lines per row, rows per unit
+    int lc = 0, rc = 0, ul = 0;  // line within the row, row within the unit, units left
+    const char* cur = nullptr;   // current weight line
+    const char* scur = nullptr;  // its side values
+    // Pointer steps: every line moves on by one line; a row's end adds drow, a unit's end adds dunit on top, so
+    // the common step is two 64-bit adds and a counter (the loader issues one line per slot, and a wave issues
+    // one instruction per 4 cycles, so this bookkeeping bounds the streaming rate of a loader wave).
+    long drow = 0, dunit = 0, sdrow = 0, sdunit = 0;
+    int sline = 0;
 
     __device__ void set_seg() {
         const char* mat;
@@ -317,14 +321,17 @@ struct Stream {
             cols = seg == 3 ? INTER : H;
         }
         lpr = cols / Fmt<WT>::CPC / kWave;
-        const size_t rb = row_bytes<WT>(cols);
-        const size_t sb = WT == WType::INT4 ? (cols / 128) * kScB : kScB;  // side bytes per row
-        kstr = krows * rb, ustr = urows * rb;
-        skstr = krows * sb, sustr = urows * sb;
-        sline = WT == WType::INT4 ? 16 * kScB : 0;  // an int4 line spans 16 scale groups
-        unitp = rowp = cur = mat + static_cast<size_t>(r0) * rb;
-        sunitp = srowp = scur = sc + static_cast<size_t>(r0) * sb;
-        lc = lpr, rl = rpu, ul = (N - gw + NW - 1) / NW;
+        const long rb = static_cast<long>(row_bytes<WT>(cols));
+        const long sb = WT == WType::INT4 ? (cols / 128) * static_cast<long>(kScB) : static_cast<long>(kScB);  // side bytes per row
+        sline = WT == WType::INT4 ? 16 * static_cast<int>(kScB) : 0;  // an int4 line spans 16 scale groups
+        const long kstr = krows * rb, ustr = urows * rb, skstr = krows * sb, sustr = urows * sb;
+        drow = kstr - lpr * 1024L;
+        sdrow = skstr - lpr * static_cast<long>(sline);
+        dunit = ustr - rpu * kstr;
+        sdunit = sustr - rpu * skstr;
+        cur = mat + static_cast<size_t>(r0) * rb;
+        scur = sc + static_cast<size_t>(r0) * sb;
+        lc = 0, rc = 0, ul = (N - gw + NW - 1) / NW;
         have = ul > 0;
     }
     // Next segment (each wave has units in every segment when NW <= kPairs).
@@ -349,30 +356,20 @@ struct Stream {
         p = pp, gw = gw_, NW = nw, l = 0, seg = 0, end = false;
         set_seg();
     }
-    // Step past the current line within the segment; clears `have` at the segment's end.
+    // Step past the current line within the segment; clears `have` at the segment's end (cur then points past the
+    // segment and is not loaded again: the loader repeats its last line instead).
     __device__ __forceinline__ void advance() {
-        if (--lc > 0) {
-            cur += 1024;
-            scur += sline;
-            return;
-        }
-        lc = lpr;
-        if (--rl > 0) {
-            rowp += kstr;
-            srowp += skstr;
-        } else {
-            rl = rpu;
-            if (--ul == 0) {
-                have = false;
-                return;
-            }
-            unitp += ustr;
-            sunitp += sustr;
-            rowp = unitp;
-            srowp = sunitp;
-        }
-        cur = rowp;
-        scur = srowp;
+        cur += 1024;
+        scur += sline;
+        if (++lc < lpr) return;
+        lc = 0;
+        cur += drow;
+        scur += sdrow;
+        if (++rc < rpu) return;
+        rc = 0;
+        cur += dunit;
+        scur += sdunit;
+        if (--ul == 0) have = false;
     }
 };
 
@@ -415,7 +412,7 @@ __device__ __forceinline__ void loader(const DecodeParams& p, Smem<WT>& sm, int 
     };
 #pragma unroll
     for (int s = 0; s < C::NB; ++s) issue(s);
-    int k = 0, cdone = 0;
+    int k = 0, cdone = 0, slot = 0;  // slot = k mod S, kept as a counter
     bool lbad = false;
     for (;;) {
         bool any = false;
@@ -430,10 +427,10 @@ __device__ __forceinline__ void loader(const DecodeParams& p, Smem<WT>& sm, int 
                         if (k - cdone < C::S || lds_give_up(spins, lbad)) break;
                     }
                 }
-                const int slot = k % C::S;
                 sm.ring[wave][slot][lane] = buf[s];
                 if constexpr (C::kQuant) sm.side[wave][slot][lane] = side_value<WT>(sd[s]);
                 ++k;
+                slot = slot + 1 == C::S ? 0 : slot + 1;
                 if (lane == 0) lds_store(&sm.full[wave], k);
             }
             issue(s);
@@ -889,6 +886,87 @@ __device__ __forceinline__ float down_dot_dig8(Smem<WType::INT8>& sm, Cons& cs, 
     }
     const float t = fmaf(fmaf(static_cast<float>(a2), 256.f, static_cast<float>(a1)), 256.f, static_cast<float>(a0));
     return wave_sum(t) * sc * rs;
+}
+
+// The wave's two down rows r and r + NW at once (ring lines k .. k + 4 LPR8 - 1 in row order): the digit words of
+// each column group are read from the table once for both rows, which halves the phase's LDS reads (six digit
+// words per weight word).  Same arithmetic per row as down_dot_dig4 / down_dot_dig8.
+__device__ __forceinline__ void down_dot2_dig4(Smem<WType::INT4>& sm, Cons& cs, const uint32_t* tab, float sc, int wave,
+                                               int lane, bool& lbad, float& d0, float& d1) {
+    using C = RingCfg<WType::INT4>;
+    static_assert(C::LPR8 == 4 && C::S >= 8, "two int4 down rows fit the ring");
+    ring_wait(cs.k + 8, cs.cfull, &sm.full[wave], lbad);
+    u32x4 w[2][4];
+    float gs[2][4];
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            w[q][g] = sm.ring[wave][(cs.k + 4 * q + g) % C::S][lane];
+            gs[q][g] = sm.side[wave][(cs.k + 4 * q + g) % C::S][lane];
+        }
+    float s[2] = {0.f, 0.f};
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const uint32_t* t = tab + (g * kWave + lane) * 4;
+        u32x4 d[6];
+#pragma unroll
+        for (int k = 0; k < 6; ++k) d[k] = *reinterpret_cast<const u32x4*>(t + k * kDownWords);
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            int a[6] = {0, 0, 0, 0, 0, 0};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int wq = static_cast<int>(w[q][g][i] ^ 0x88888888u);
+#pragma unroll
+                for (int k = 0; k < 6; ++k) a[k] = __builtin_amdgcn_sdot8(wq, static_cast<int>(d[k][i]), a[k], false);
+            }
+            const int p0 = a[0] + 16 * a[1], p1 = a[2] + 16 * a[3], p2 = a[4] + 16 * a[5];
+            s[q] = fmaf(fmaf(static_cast<float>(p2), 65536.f, static_cast<float>(p0 + 256 * p1)), gs[q][g], s[q]);
+        }
+    }
+    cs.k += 8;
+    release(sm, cs, wave, lane);
+    d0 = wave_sum(s[0]) * sc;
+    d1 = wave_sum(s[1]) * sc;
+}
+
+__device__ __forceinline__ void down_dot2_dig8(Smem<WType::INT8>& sm, Cons& cs, const uint32_t* tab, float sc, int wave,
+                                               int lane, bool& lbad, float& d0, float& d1) {
+    using C = RingCfg<WType::INT8>;
+    static_assert(C::LPR8 == 8 && C::S >= 16, "two int8 down rows fit the ring");
+    ring_wait(cs.k + 16, cs.cfull, &sm.full[wave], lbad);
+    int a[2][3] = {{0, 0, 0}, {0, 0, 0}};
+    const float rs0 = sm.side[wave][cs.k % C::S][lane], rs1 = sm.side[wave][(cs.k + 8) % C::S][lane];
+#pragma unroll
+    for (int c0 = 0; c0 < 8; c0 += 4) {
+        u32x4 w[2][4];
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) w[q][g] = sm.ring[wave][(cs.k + 8 * q + c0 + g) % C::S][lane];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const uint32_t* t = tab + ((c0 + g) * kWave + lane) * 4;
+            const u32x4 e0 = *reinterpret_cast<const u32x4*>(t), e1 = *reinterpret_cast<const u32x4*>(t + 2 * kDownWords),
+                        e2 = *reinterpret_cast<const u32x4*>(t + 4 * kDownWords);
+#pragma unroll
+            for (int q = 0; q < 2; ++q)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int wi = static_cast<int>(w[q][g][i]);
+                    a[q][0] = __builtin_amdgcn_sdot4(wi, static_cast<int>(e0[i]), a[q][0], false);
+                    a[q][1] = __builtin_amdgcn_sdot4(wi, static_cast<int>(e1[i]), a[q][1], false);
+                    a[q][2] = __builtin_amdgcn_sdot4(wi, static_cast<int>(e2[i]), a[q][2], false);
+                }
+        }
+    }
+    cs.k += 16;
+    release(sm, cs, wave, lane);
+    const float t0 = fmaf(fmaf(static_cast<float>(a[0][2]), 256.f, static_cast<float>(a[0][1])), 256.f, static_cast<float>(a[0][0]));
+    const float t1 = fmaf(fmaf(static_cast<float>(a[1][2]), 256.f, static_cast<float>(a[1][1])), 256.f, static_cast<float>(a[1][0]));
+    d0 = wave_sum(t0) * sc * rs0;
+    d1 = wave_sum(t1) * sc * rs1;
 }
 
 // Per-chunk sums of the lane's down-projection inputs (the bias correction of quantised chunks);
@@ -1564,8 +1642,29 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
             stamp_in(p, l, 5, 1);
             drain();
             int k = wave * kRPW;
+            int r = gw;
+            if constexpr (kDig) {
 #pragma unroll 1
-            for (int r = gw; r < H; r += NW, ++k) {
+                for (; r + NW < H; r += 2 * NW, k += 2) {
+                    float d0, d1;
+                    if constexpr (WT == WType::INT4) {
+                        down_dot2_dig4(sm, cs, reinterpret_cast<const uint32_t*>(sm.big), dsc, wave, lane, lbad, d0, d1);
+                    } else {
+                        down_dot2_dig8(sm, cs, reinterpret_cast<const uint32_t*>(sm.big), dsc, wave, lane, lbad, d0, d1);
+                    }
+                    if (lane == 0) {
+                        const float x0 = sm.ares[k] + d0, x1 = sm.ares[k + 1] + d1;
+                        tstore(txo + r, x0, tg + T_X);
+                        tstore(txo + r + NW, x1, tg + T_X);
+                        if (p.residuals) {
+                            *glob(p.residuals + static_cast<size_t>(l + 1) * H + r) = x0;
+                            *glob(p.residuals + static_cast<size_t>(l + 1) * H + r + NW) = x1;
+                        }
+                    }
+                }
+            }
+#pragma unroll 1
+            for (; r < H; r += NW, ++k) {
                 float d;
                 if constexpr (WT == WType::INT4) {
                     d = down_dot_dig4(sm, cs, reinterpret_cast<const uint32_t*>(sm.big), dsc, wave, lane, lbad);
