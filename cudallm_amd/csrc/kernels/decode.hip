@@ -28,6 +28,7 @@
 //    Indices never depend on activation values and the token is clamped, so no access can leave
 //    its buffer even then.  The host reports the flag as a device error.
 #include "../decode.h"
+#include "../decode_walk.h"
 #include "../kernels.h"
 #include "device.h"
 #include "dot.h"
@@ -66,6 +67,8 @@ constexpr int kPairs = QKV / 2;          // RoPE pairs (i, i+32) of every q/k/v 
 #define CLLM_LM_ROWS 2
 #endif
 constexpr int kLmR = CLLM_LM_ROWS;       // lm_head rows per unit
+static_assert(walk::kH == H && walk::kInter == INTER && walk::kVocab == VOCAB && walk::kPairs == kPairs,
+              "the weight walk and the kernel agree on the shapes");
 static_assert(VOCAB % kLmR == 0, "lm_head units");
 
 enum : unsigned { T_QKV = 0, T_ATT_PART = 1, T_ATT = 2, T_XA = 3, T_ACT = 4, T_X = 5 };
@@ -285,54 +288,24 @@ __device__ __forceinline__ void ring_wait(int need, int& cfull, int* full, bool&
 // All state is wave-uniform.
 template <WType WT>
 struct Stream {
-    using C = RingCfg<WT>;
-    static constexpr size_t kScB = WT == WType::INT4 ? 2 : 4;  // bytes per scale
     const DecodeParams* p;
     int gw, NW;
     int l = 0, seg = 0;
-    bool have = false, end = false;
-    int lpr = 1, rpu = 1;        // lines per row, rows per unit
-    int lc = 0, rc = 0, ul = 0;  // line within the row, row within the unit, units left
-    const char* cur = nullptr;   // current weight line
-    const char* scur = nullptr;  // its side values
-    // Pointer steps: every line moves on by one line; a row's end adds drow, a unit's end adds dunit on top, so
-    // the common step is two 64-bit adds and a counter (the loader issues one line per slot, and a wave issues
-    // one instruction per 4 cycles, so this bookkeeping bounds the streaming rate of a loader wave).
-    long drow = 0, dunit = 0, sdrow = 0, sdunit = 0;
-    int sline = 0;
+    bool end = false;
+    walk::Walker<const char*> w;  // the segment's lines (decode_walk.h)
 
     __device__ void set_seg() {
         const char* mat;
         const char* sc;
-        int N, r0, krows, urows, cols;
         if (seg == 4) {
             mat = static_cast<const char*>(p->emb);
             sc = static_cast<const char*>(p->emb_s);
-            N = VOCAB / kLmR, r0 = gw * kLmR, krows = 1, urows = NW * kLmR, rpu = kLmR, cols = H;
         } else {
             const DecodeLayer L = load_layer(p->layers, l);
             mat = static_cast<const char*>(seg == 0 ? L.wqkv : seg == 1 ? L.wo : seg == 2 ? L.wgu : L.wd);
             sc = static_cast<const char*>(seg == 0 ? L.sqkv : seg == 1 ? L.so : seg == 2 ? L.sgu : L.sd);
-            N = seg == 0 ? kPairs : seg == 2 ? INTER : H;
-            r0 = seg == 0 ? (gw / 32) * HD + gw % 32 : gw;
-            krows = seg == 0 ? 32 : seg == 2 ? INTER : 0;
-            urows = seg == 0 ? 2 * NW : NW;
-            rpu = (seg == 0 || seg == 2) ? 2 : 1;
-            cols = seg == 3 ? INTER : H;
         }
-        lpr = cols / Fmt<WT>::CPC / kWave;
-        const long rb = static_cast<long>(row_bytes<WT>(cols));
-        const long sb = WT == WType::INT4 ? (cols / 128) * static_cast<long>(kScB) : static_cast<long>(kScB);  // side bytes per row
-        sline = WT == WType::INT4 ? 16 * static_cast<int>(kScB) : 0;  // an int4 line spans 16 scale groups
-        const long kstr = krows * rb, ustr = urows * rb, skstr = krows * sb, sustr = urows * sb;
-        drow = kstr - lpr * 1024L;
-        sdrow = skstr - lpr * static_cast<long>(sline);
-        dunit = ustr - rpu * kstr;
-        sdunit = sustr - rpu * skstr;
-        cur = mat + static_cast<size_t>(r0) * rb;
-        scur = sc + static_cast<size_t>(r0) * sb;
-        lc = 0, rc = 0, ul = (N - gw + NW - 1) / NW;
-        have = ul > 0;
+        w.start(walk::seg_of(WT, seg, gw, NW, kLmR), mat, sc);
     }
     // Next segment (each wave has units in every segment when NW <= kPairs).
     __device__ void next_seg() {
@@ -355,21 +328,6 @@ struct Stream {
     __device__ void init(const DecodeParams* pp, int gw_, int nw) {
         p = pp, gw = gw_, NW = nw, l = 0, seg = 0, end = false;
         set_seg();
-    }
-    // Step past the current line within the segment; clears `have` at the segment's end (cur then points past the
-    // segment and is not loaded again: the loader repeats its last line instead).
-    __device__ __forceinline__ void advance() {
-        cur += 1024;
-        scur += sline;
-        if (++lc < lpr) return;
-        lc = 0;
-        cur += drow;
-        scur += sdrow;
-        if (++rc < rpu) return;
-        rc = 0;
-        cur += dunit;
-        scur += sdunit;
-        if (--ul == 0) have = false;
     }
 };
 
@@ -397,18 +355,18 @@ __device__ __forceinline__ void loader(const DecodeParams& p, Smem<WT>& sm, int 
     u32x4 buf[C::NB];
     uint32_t sd[C::NB];
     bool v[C::NB];
-    const char* last = st.cur;
-    const char* slast = st.scur;
+    const char* last = st.w.cur;
+    const char* slast = st.w.scur;
     auto issue = [&](int s) {
-        v[s] = st.have;
-        if (st.have) {
-            last = st.cur;
-            slast = st.scur;
+        v[s] = st.w.have;
+        if (st.w.have) {
+            last = st.w.cur;
+            slast = st.w.scur;
         }
         buf[s] = load_stream(last + loff);
         if constexpr (WT == WType::INT8) sd[s] = gload(reinterpret_cast<const uint32_t*>(slast));
         if constexpr (WT == WType::INT4) sd[s] = gload(reinterpret_cast<const uint16_t*>(slast + soff));
-        if (st.have) st.advance();
+        if (st.w.have) st.w.advance();
     };
 #pragma unroll
     for (int s = 0; s < C::NB; ++s) issue(s);
@@ -435,7 +393,7 @@ __device__ __forceinline__ void loader(const DecodeParams& p, Smem<WT>& sm, int 
             }
             issue(s);
         }
-        if (!st.have && !st.end) {
+        if (!st.w.have && !st.end) {
             stall_at(p, kStallLoader);
             st.next_seg();
         }
