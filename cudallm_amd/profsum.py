@@ -1,6 +1,6 @@
 """Summaries of rocprofv3 output for this library's kernels (the tables under profiles/).
 
-    python -m cudallm_amd.profsum trace DIR [--matvec-blocks] [--decode]
+    python -m cudallm_amd.profsum trace DIR [--matvec-blocks WTYPE] [--decode [--skip N] [--take K]]
     python -m cudallm_amd.profsum counters FETCH_DIR WRITE_DIR [--calib-bytes N]
 
 ``trace``: reads DIR/*kernel_trace.csv (rocprofv3 --kernel-trace).  With --matvec-blocks the matvec dispatches are
@@ -74,17 +74,19 @@ def matvec_blocks(rows, wtype: str):
 PROBE_US = 50.0  # the engine's co-residency probe launch of the decode kernel takes a few microseconds
 
 
-def decode_stats(rows):
-    """Decode steps per weight type; the co-residency probe launches (same kernel, under PROBE_US) are counted
-    apart."""
+def decode_stats(rows, skip: int = 0, take: int = 0):
+    """Decode steps per weight type, in dispatch order; the co-residency probe launches (same kernel, under PROBE_US)
+    are counted apart.  `skip` drops each weight type's first steps and `take` (when > 0) keeps the next `take`:
+    bench.py's timed region is steps PROMPT + warmup + 1 .. + steps (skip = 16 + warmup, take = steps)."""
     per, probes = {}, {}
-    for r in rows:
+    for r in sorted(rows, key=lambda r: int(r["Start_Timestamp"])):
         if "decode_kernel" not in r["Kernel_Name"]:
             continue
         wd = _dtype(r["Kernel_Name"])
         us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
         (probes if us < PROBE_US else per).setdefault(wd, []).append(us)
-    out = {wd: _stats(us) for wd, us in per.items()}
+    per = {wd: us[skip:skip + take] if take > 0 else us[skip:] for wd, us in per.items()}
+    out = {wd: _stats(us) for wd, us in per.items() if us}
     for wd, us in probes.items():
         out.setdefault(wd, {})["probe_launches"] = len(us)
     return out
@@ -125,6 +127,8 @@ def main(argv=None) -> int:
     t.add_argument("dir", type=Path)
     t.add_argument("--matvec-blocks", metavar="WTYPE")
     t.add_argument("--decode", action="store_true")
+    t.add_argument("--skip", type=int, default=0, help="decode: drop each weight type's first N steps")
+    t.add_argument("--take", type=int, default=0, help="decode: then keep N steps (0 = all)")
     c = sub.add_parser("counters")
     c.add_argument("fetch_dir", type=Path)
     c.add_argument("write_dir", type=Path)
@@ -136,7 +140,7 @@ def main(argv=None) -> int:
         if args.matvec_blocks:
             res["matvec"] = matvec_blocks(rows, args.matvec_blocks)
         if args.decode:
-            res["decode"] = decode_stats(rows)
+            res["decode"] = decode_stats(rows, args.skip, args.take)
     else:
         res = counters(args.fetch_dir, args.write_dir, args.calib_bytes)
     print(json.dumps(res, indent=1))
