@@ -53,7 +53,7 @@ constexpr unsigned kLdsSpinCap = 1u << 26;  // bounded waits inside the workgrou
 constexpr int kPartStride = HD + 2;      // o[64], m, l
 constexpr int kPairs = QKV / 2;          // RoPE pairs (i, i+32) of every q/k/v head
 // Tuning knobs of the decode kernel, overridable at build time (cudallm_amd/sweep_decode.py sweeps them): lines in
-// flight per loader wave, ring slots per compute wave (bf16 / quantised), lm_head rows per unit.
+// flight per loader wave, ring slots per compute wave and lm_head rows per unit (each for bf16 / quantised).
 #ifndef CLLM_LOADER_LINES
 #define CLLM_LOADER_LINES 16
 #endif
@@ -61,15 +61,19 @@ constexpr int kPairs = QKV / 2;          // RoPE pairs (i, i+32) of every q/k/v 
 #define CLLM_RING_SLOTS_BF16 30
 #endif
 #ifndef CLLM_RING_SLOTS_QUANT
-#define CLLM_RING_SLOTS_QUANT 20
+#define CLLM_RING_SLOTS_QUANT 22
 #endif
-#ifndef CLLM_LM_ROWS
-#define CLLM_LM_ROWS 2
+#ifndef CLLM_LM_ROWS_BF16
+#define CLLM_LM_ROWS_BF16 2
 #endif
-constexpr int kLmR = CLLM_LM_ROWS;       // lm_head rows per unit
+#ifndef CLLM_LM_ROWS_QUANT
+#define CLLM_LM_ROWS_QUANT 4
+#endif
+template <WType WT>
+constexpr int kLmR = WT == WType::BF16 ? CLLM_LM_ROWS_BF16 : CLLM_LM_ROWS_QUANT;  // lm_head rows per unit
 static_assert(walk::kH == H && walk::kInter == INTER && walk::kVocab == VOCAB && walk::kPairs == kPairs,
               "the weight walk and the kernel agree on the shapes");
-static_assert(VOCAB % kLmR == 0, "lm_head units");
+static_assert(VOCAB % kLmR<WType::BF16> == 0 && VOCAB % kLmR<WType::INT8> == 0, "lm_head units");
 
 enum : unsigned { T_QKV = 0, T_ATT_PART = 1, T_ATT = 2, T_XA = 3, T_ACT = 4, T_X = 5 };
 constexpr unsigned T_ARG = NL * kTagStride;
@@ -305,7 +309,7 @@ struct Stream {
             mat = static_cast<const char*>(seg == 0 ? L.wqkv : seg == 1 ? L.wo : seg == 2 ? L.wgu : L.wd);
             sc = static_cast<const char*>(seg == 0 ? L.sqkv : seg == 1 ? L.so : seg == 2 ? L.sgu : L.sd);
         }
-        w.start(walk::seg_of(WT, seg, gw, NW, kLmR), mat, sc);
+        w.start(walk::seg_of(WT, seg, gw, NW, kLmR<WT>), mat, sc);
     }
     // Next segment (each wave has units in every segment when NW <= kPairs).
     __device__ void next_seg() {
@@ -1687,13 +1691,13 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
         // read (the take-ahead form held the next unit's rows across the iteration, the pattern that gave
         // layout-dependent wrong results in gate_up).
 #pragma unroll 1
-        for (int u = gw; u < VOCAB / kLmR; u += NW) {
-            Row<WT> rr[kLmR];
+        for (int u = gw; u < VOCAB / kLmR<WT>; u += NW) {
+            Row<WT> rr[kLmR<WT>];
 #pragma unroll
-            for (int i = 0; i < kLmR; ++i) take_row<WT>(sm, cs, wave, lane, lbad, rr[i]);
-            float d[kLmR];
+            for (int i = 0; i < kLmR<WT>; ++i) take_row<WT>(sm, cs, wave, lane, lbad, rr[i]);
+            float d[kLmR<WT>];
 #pragma unroll
-            for (int i = 0; i < kLmR; ++i) {
+            for (int i = 0; i < kLmR<WT>; ++i) {
                 if constexpr (kDig) {
                     d[i] = row_dot_dig<WT>(rr[i], dg, dsc);
                 } else {
@@ -1702,8 +1706,8 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
             }
             release(sm, cs, wave, lane);
 #pragma unroll
-            for (int i = 0; i < kLmR; ++i) {
-                const int r = u * kLmR + i;
+            for (int i = 0; i < kLmR<WT>; ++i) {
+                const int r = u * kLmR<WT> + i;
                 if (lane == nrow + i) {
                     lg = d[i];
                     lr = r;
@@ -1713,7 +1717,7 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
                     bi = r;
                 }
             }
-            nrow += kLmR;
+            nrow += kLmR<WT>;
             if (nrow == kWave) {  // wave-uniform: a branch, so the drain below runs only here
                 *glob(p.logits + lr) = lg;
                 drain();  // nothing left pending for the hot path
