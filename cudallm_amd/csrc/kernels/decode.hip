@@ -520,10 +520,18 @@ static_assert(Dig<WType::INT8>::ND * Dig<WType::INT8>::WPD == Dig<WType::INT4>::
               "digit tables share one size");
 static_assert(Dig<WType::INT8>::ND * Dig<WType::INT8>::WPD == kDigWordsMax, "digit table size");
 
-// Exponent e of the fixed-point scale from a bound m >= max |x^|: m 2^e < 2^22.
+// Exponent e of the fixed-point scale from a bound m >= max |x^|: m 2^e < 2^22.  At most 126, so that 2^e and 2^-e
+// are normal floats (inputs below 2^-104 then keep fewer bits, which changes nothing measurable).
 __device__ __forceinline__ int dig_exponent(float m) {
     if (!(m > 0.f) || !(m < INFINITY)) return 0;
-    return 21 - ilogbf(m);
+    return min(21 - ilogbf(m), 126);
+}
+
+// The offset fixed-point word (xi + C) mod 2^32 of xi = rint(v 2^e), from one FMA: v 2^e + 1.5 2^23 lands in
+// [2^23, 2^24), where the float's bit pattern is 0x4B400000 + xi, rounded to nearest even like rintf.  The xor
+// with C that makes the digits signed is applied to the packed digit words instead (every digit's top bit).
+__device__ __forceinline__ uint32_t fixed_word(float v, float scale, uint32_t C) {
+    return __builtin_bit_cast(uint32_t, fmaf(v, scale, 12582912.f)) + (C - 0x4B400000u);
 }
 
 // Byte planes of four 24-bit words: P[j] byte i = byte j of a_i (v_perm_b32 picks bytes of {s0, s1}; selector
@@ -564,13 +572,13 @@ __device__ void make_digits(const float* x, const Norm8& gn, float inv, int e, u
     using D = Dig<WT>;
     const f32x4 x0 = reinterpret_cast<const f32x4*>(x)[2 * tid], x1 = reinterpret_cast<const f32x4*>(x)[2 * tid + 1];
     const f32x4 g0 = gn.g0, g1 = gn.g1;
+    const float scale = ldexpf(1.f, e);
     uint32_t u[8];
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
         const float xc = c < 4 ? x0[c] : x1[c - 4];
         const float gc = c < 4 ? g0[c] : g1[c - 4];
-        const int xi = static_cast<int>(rintf(ldexpf(xc * inv * gc, e)));
-        u[c] = (static_cast<uint32_t>(xi) + D::C) ^ D::C;
+        u[c] = fixed_word(xc * inv * gc, scale, D::C);
     }
     if constexpr (WT == WType::INT8) {
         uint32_t P[2][3];
@@ -579,12 +587,12 @@ __device__ void make_digits(const float* x, const Norm8& gn, float inv, int e, u
 #pragma unroll
         for (int k = 0; k < 3; ++k)
 #pragma unroll
-            for (int h = 0; h < 2; ++h) tab[k * D::WPD + 2 * tid + h] = P[h][k];
+            for (int h = 0; h < 2; ++h) tab[k * D::WPD + 2 * tid + h] = P[h][k] ^ 0x80808080u;
     } else {
         uint32_t w[6];
         nibble_words(u, w);
 #pragma unroll
-        for (int k = 0; k < 6; ++k) tab[k * D::WPD + tid] = w[k];
+        for (int k = 0; k < 6; ++k) tab[k * D::WPD + tid] = w[k] ^ 0x88888888u;
     }
 }
 
@@ -750,17 +758,17 @@ __device__ __forceinline__ void down_digits(const float* a, int e, int tid, uint
     static_assert(INTER / 8 / kCT == 4, "four column groups per thread");
     static_assert(6 * kDownWords <= kBig, "the digit table fits where the inputs were");
     constexpr uint32_t C = 0x888888u;
+    const float scale = ldexpf(1.f, e);
 #pragma unroll
     for (int j = 0; j < INTER / 8 / kCT; ++j) {
         const int m = tid + kCT * j;
         const f32x4 x0 = reinterpret_cast<const f32x4*>(a)[2 * m], x1 = reinterpret_cast<const f32x4*>(a)[2 * m + 1];
         uint32_t u[8];
 #pragma unroll
-        for (int c = 0; c < 8; ++c) {
-            const float xc = c < 4 ? x0[c] : x1[c - 4];
-            u[c] = (static_cast<uint32_t>(static_cast<int>(rintf(ldexpf(xc, e)))) + C) ^ C;
-        }
+        for (int c = 0; c < 8; ++c) u[c] = fixed_word(c < 4 ? x0[c] : x1[c - 4], scale, C);
         nibble_words(u, dw[j]);
+#pragma unroll
+        for (int k = 0; k < 6; ++k) dw[j][k] ^= 0x88888888u;
     }
 }
 
@@ -804,23 +812,21 @@ __device__ __forceinline__ float down_dot_dig4(Smem<WType::INT4>& sm, Cons& cs, 
 // tab[k * 2048 + m], so a down row's line c gives lane l the words m = 256 c + 4 l + i.
 __device__ __forceinline__ void down_digits8(const float* a, int e, int tid, uint32_t (&dw)[4][6]) {
     constexpr uint32_t C = 0x808080u;
+    const float scale = ldexpf(1.f, e);
 #pragma unroll
     for (int j = 0; j < INTER / 8 / kCT; ++j) {
         const int m = tid + kCT * j;
         const f32x4 x0 = reinterpret_cast<const f32x4*>(a)[2 * m], x1 = reinterpret_cast<const f32x4*>(a)[2 * m + 1];
         uint32_t u[8];
 #pragma unroll
-        for (int c = 0; c < 8; ++c) {
-            const float xc = c < 4 ? x0[c] : x1[c - 4];
-            u[c] = (static_cast<uint32_t>(static_cast<int>(rintf(ldexpf(xc, e)))) + C) ^ C;
-        }
+        for (int c = 0; c < 8; ++c) u[c] = fixed_word(c < 4 ? x0[c] : x1[c - 4], scale, C);
         uint32_t P[2][3];
         byte_planes(u[0], u[1], u[2], u[3], P[0]);
         byte_planes(u[4], u[5], u[6], u[7], P[1]);
 #pragma unroll
         for (int k = 0; k < 3; ++k)
 #pragma unroll
-            for (int h = 0; h < 2; ++h) dw[j][2 * k + h] = P[h][k];
+            for (int h = 0; h < 2; ++h) dw[j][2 * k + h] = P[h][k] ^ 0x80808080u;
     }
 }
 
