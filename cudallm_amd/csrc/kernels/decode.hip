@@ -1153,7 +1153,8 @@ template <WType WT>
 __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
     using F = Fmt<WT>;
     constexpr int NX = F::CPL * F::CPC;
-    constexpr bool kDig = WT != WType::BF16;  // gate_up and lm_head use the integer dot products
+    constexpr bool kDig = WT != WType::BF16;  // gate_up, down and lm_head use the integer dot products
+    constexpr bool kQkvDig = WT == WType::INT8;  // and int8's qkv
     __shared__ Smem<WT> sm;
 
     if (threadIdx.x < kCW) {
@@ -1217,14 +1218,22 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
 
     stamp(p, 0);
     {
-        float ss = 0.f;
+        // The embedding row is layer 0's qkv input: its sum of squares, and for int8 max |x g| (g: layer 0's
+        // attn_norm), which the digit prologue of the qkv phase takes as fetch() leaves it for later layers.
+        [[maybe_unused]] const float* g0 = kQkvDig ? load_layer(p.layers, 0).attn_norm : nullptr;
+        float ss = 0.f, mx = 0.f;
         for (int j = tid; j < H; j += kCT) {
             const float x = embed<WT>(p.emb, p.emb_s, tok, j);
             sm.big[kXin<WT> + j] = x;
             ss += x * x;
+            if constexpr (kQkvDig) mx = fmaxf(mx, fabsf(x * gload(g0 + j)));
         }
         ss = wave_sum(ss);
         if (lane == 0) sm.part[wave] = ss;
+        if constexpr (kQkvDig) {
+            mx = wave_max(mx);
+            if (lane == 0) sm.pmax[wave] = mx;
+        }
     }
     if (tid < HD / 2) {  // the angles depend only on the position: one sincos per pair per step
         float sn, csn;
@@ -1250,21 +1259,44 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
         // ---- qkv (+ attn_norm prologue, RoPE, fp16 KV write); unit = RoPE pair (i, i+32) of a head ----
         renew();
         {
+            // int8 uses the integer digit dots here too (the digit prologue is about 60 instructions per thread; each
+            // row then costs about 40 instead of about 85): int8 -5 us per step.  int4 measured +3 us with them (its
+            // float rows were already cheaper than int8's), so it keeps the float path.
             NormW<WT> nw;
-            load_norm<WT>(Lw.attn_norm, lane, nw);
-            stall_at(p, kStallQkv);
-            if (l > 0) {
-                if constexpr (!kDig) cbar(sm.bar, ep, wave, lane, lbad);  // every wave is done with the down input
-                fetch<H, true>(p.tx + static_cast<size_t>(l) * H, tg - kTagStride + T_X, sm.big + kXin<WT>, sm.part, err, tid);
+            float xr[kQkvDig ? 1 : NX], xsum = 0.f;
+            Dig<WT> dg;
+            float dsc = 0.f;
+            if constexpr (kQkvDig) {
+                const Norm8 gn = load_norm8(Lw.attn_norm, tid);
+                stall_at(p, kStallQkv);
+                if (l > 0) {
+                    fetch<H, true, 0, 1>(p.tx + static_cast<size_t>(l) * H, tg - kTagStride + T_X, sm.big + kXin<WT>,
+                                         sm.part, err, tid, Lw.attn_norm, sm.pmax);
+                    cbar(sm.bar, ep, wave, lane, lbad);
+                }
+                stamp_in(p, l, 0, 0);
+                stall_at(p, kStallInputs);
+                const float inv = rms_inv(sm.part, p.eps);
+                dsc = digits_prologue<WT>(sm, inv, gn, tid, sm.big + kXin<WT>);
+                if (lane < kRPW && gw + lane * NW < H) sm.xres[wave * kRPW + lane] = sm.big[kXin<WT> + gw + lane * NW];
                 cbar(sm.bar, ep, wave, lane, lbad);
+                load_digits<WT>(reinterpret_cast<const uint32_t*>(sm.big + kDigOff), lane, dg);
+            } else {
+                load_norm<WT>(Lw.attn_norm, lane, nw);
+                stall_at(p, kStallQkv);
+                if (l > 0) {
+                    if constexpr (!kDig) cbar(sm.bar, ep, wave, lane, lbad);  // every wave is done with the down input
+                    fetch<H, true>(p.tx + static_cast<size_t>(l) * H, tg - kTagStride + T_X, sm.big + kXin<WT>, sm.part, err,
+                                   tid);
+                    cbar(sm.bar, ep, wave, lane, lbad);
+                }
+                stamp_in(p, l, 0, 0);
+                stall_at(p, kStallInputs);
+                const float inv = rms_inv(sm.part, p.eps);
+                lane_inputs<WT, true>(sm.big + kXin<WT>, &nw, inv, xr, xsum, lane);
+                if (lane < kRPW && gw + lane * NW < H) sm.xres[wave * kRPW + lane] = sm.big[kXin<WT> + gw + lane * NW];
             }
-            stamp_in(p, l, 0, 0);
-            stall_at(p, kStallInputs);
-            const float inv = rms_inv(sm.part, p.eps);
-            float xr[NX], xsum;
-            lane_inputs<WT, true>(sm.big + kXin<WT>, &nw, inv, xr, xsum, lane);
-            if (lane < kRPW && gw + lane * NW < H) sm.xres[wave * kRPW + lane] = sm.big[kXin<WT> + gw + lane * NW];
-            ep_in = carrive(sm.bar, ep, wave, lane);  // the attention tiles may now overwrite the input
+            ep_in = carrive(sm.bar, ep, wave, lane);  // the attention tiles may now overwrite the input / digit table
             stamp_in(p, l, 0, 1);
             drain();
 #pragma unroll 1
@@ -1272,8 +1304,14 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
                 Row<WT> ra, rb;
                 take_row<WT>(sm, cs, wave, lane, lbad, ra);
                 take_row<WT>(sm, cs, wave, lane, lbad, rb);
-                const float d0 = row_dot<WT>(ra, xr, xsum);
-                const float d1 = row_dot<WT>(rb, xr, xsum);
+                float d0, d1;
+                if constexpr (kQkvDig) {
+                    d0 = row_dot_dig<WT>(ra, dg, dsc);
+                    d1 = row_dot_dig<WT>(rb, dg, dsc);
+                } else {
+                    d0 = row_dot<WT>(ra, xr, xsum);
+                    d1 = row_dot<WT>(rb, xr, xsum);
+                }
                 release(sm, cs, wave, lane);
                 if (lane == 0) {
                     const int h = u / 32, i = u % 32, r0 = h * HD + i;
@@ -1327,7 +1365,7 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
                             vt[k] = load_stream(Vg + static_cast<size_t>(t0 + r) * HD + c * 8);
                         }
                     }
-                    if (!kDig && first) cwait(sm.bar, ep_in, lbad);  // every wave has read the qkv input
+                    if ((!kDig || kQkvDig) && first) cwait(sm.bar, ep_in, lbad);  // every wave has read the qkv input (or its digits)
 #pragma unroll
                     for (int k = 0; k < kTile; ++k) {
                         const int idx = tid + k * kCT, r = idx / 8, c = idx % 8;
