@@ -1453,19 +1453,22 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
                     o[e] += __shfl_xor(o[e], 32);
                 }
                 const int h = kvh * 4 + wave;
-                if (g == 0) {
-                    if (nsplit == 1) {
-                        const float il = 1.f / lsum;
+                // Every lane holds its column group's 8 sums; lane j takes column j (element j % 8 of group j / 8,
+                // from lane j / 8), so the wave writes its 64 outputs with one store: whole 64-byte lines.
+                float oj = 0.f;
 #pragma unroll
-                        for (int e = 0; e < 8; ++e) tstore(tatt + h * HD + c * 8 + e, o[e] * il, tg + T_ATT);
-                    } else {
-                        uint64_t* pp = tpart + (static_cast<size_t>(h) * NS + split) * kPartStride;
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) tstore(pp + c * 8 + e, o[e], tg + T_ATT_PART);
-                        if (lane == 0) {
-                            tstore(pp + HD, m, tg + T_ATT_PART);
-                            tstore(pp + HD + 1, lsum, tg + T_ATT_PART);
-                        }
+                for (int e = 0; e < 8; ++e) {
+                    const float t = __shfl(o[e], lane >> 3);
+                    if ((lane & 7) == e) oj = t;
+                }
+                if (nsplit == 1) {
+                    tstore(tatt + h * HD + lane, oj * (1.f / lsum), tg + T_ATT);
+                } else {
+                    uint64_t* pp = tpart + (static_cast<size_t>(h) * NS + split) * kPartStride;
+                    tstore(pp + lane, oj, tg + T_ATT_PART);
+                    if (lane == 0) {
+                        tstore(pp + HD, m, tg + T_ATT_PART);
+                        tstore(pp + HD + 1, lsum, tg + T_ATT_PART);
                     }
                 }
                 stamp_attn(p, l, first, 4);
