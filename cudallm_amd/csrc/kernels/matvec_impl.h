@@ -13,6 +13,10 @@
 //  * R rows (rpb) are loaded before any is consumed, for R x (4 KiB bf16 | 2 KiB int8 | 1 KiB int4)
 //    of loads per pass; a wave issues the next pass's loads before it multiplies the current one,
 //    so up to 2R rows are in flight.
+//  * Quantised 2048-wide rows (KS = 1) use integer digit dots: each lane turns its 32 inputs into
+//    fixed-point digit words once (one scale per wave from max |x^|, the same in every wave since each
+//    covers the whole row), and a row then costs 24 v_dot8_i32_i4 / v_dot4_i32_i8 per lane instead of
+//    a conversion and an FMA per column.  The 8192-wide down rows (KS = 4) keep the float path.
 //  * Row sums are wave64 DPP butterflies (deterministic order); with KS > 1 the slice partials
 //    meet in LDS and are added in slice order.  No atomics anywhere.
 //  * The grid is persistent: min(row blocks, CUs x resident workgroups per CU).
@@ -26,6 +30,7 @@
 
 #include "../kernels.h"
 #include "device.h"
+#include "digits.h"
 #include "dot.h"
 
 namespace cllm {
@@ -53,6 +58,7 @@ __global__ void __launch_bounds__(kThreads) matvec_fast(MatvecArgs a) {
     constexpr int ROWS_WG = GROUPS * R;
     constexpr bool GLU = EP == Epilogue::SWIGLU;
     constexpr int NP = GLU ? 2 : 1;
+    constexpr bool DIG = WT != WType::BF16 && KS == 1;
     __shared__ float scratch[16];
     __shared__ float part[KS > 1 ? KS * ROWS_WG * NP : 1];
 
@@ -88,6 +94,42 @@ __global__ void __launch_bounds__(kThreads) matvec_fast(MatvecArgs a) {
             for (int e = 0; e < 4; ++e) {
                 xr[k * F::CPC + j + e] = v[e];
                 xsum += v[e];
+            }
+        }
+    }
+
+    // Digit words of the lane's inputs in its weight words' layout: int8 digit k of chunk c, word t (columns
+    // 4t .. 4t + 3) at dg[(2k + c) 4 + t]; int4 digit k of word t (columns 8t .. 8t + 7) at dg[4k + t].
+    [[maybe_unused]] uint32_t dg[DIG ? 24 : 1];
+    [[maybe_unused]] float dsc = 1.f;
+    if constexpr (DIG) {
+        float m = 0.f;
+#pragma unroll
+        for (int j = 0; j < NX; ++j) m = fmaxf(m, fabsf(xr[j]));
+        const int e = dig_exponent(wave_max(m));
+        dsc = ldexpf(1.f, -e);
+        const float scale = ldexpf(1.f, e);
+        if constexpr (WT == WType::INT8) {
+#pragma unroll
+            for (int c = 0; c < 2; ++c)
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const float* xc = xr + c * 16 + 4 * t;
+                    uint32_t P[3];
+                    byte_planes(fixed_word(xc[0], scale, 0x808080u), fixed_word(xc[1], scale, 0x808080u),
+                                fixed_word(xc[2], scale, 0x808080u), fixed_word(xc[3], scale, 0x808080u), P);
+#pragma unroll
+                    for (int k = 0; k < 3; ++k) dg[(2 * k + c) * 4 + t] = P[k] ^ 0x80808080u;
+                }
+        } else {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                uint32_t u[8], w[6];
+#pragma unroll
+                for (int b = 0; b < 8; ++b) u[b] = fixed_word(xr[8 * t + b], scale, 0x888888u);
+                nibble_words(u, w);
+#pragma unroll
+                for (int k = 0; k < 6; ++k) dg[4 * k + t] = w[k] ^ 0x88888888u;
             }
         }
     }
@@ -131,22 +173,55 @@ __global__ void __launch_bounds__(kThreads) matvec_fast(MatvecArgs a) {
         float d[R], du[R];
 #pragma unroll
         for (int i = 0; i < R; ++i) {
-            float s = 0.f, su = 0.f;
+            if constexpr (DIG) {
+                // Per lane: int8 sum_k 256^k sum(q d_k); int4 sum_k 16^k sum(q d_k) (nibble u = q + 8, so q = u xor 8)
+                // times the lane's group scale.  The row's sum times 2^-e (and the int8 row scale at the store).
+                auto dot = [&](const u32x4* v, uint16_t g) {
+                    if constexpr (WT == WType::INT8) {
+                        int a0 = 0, a1 = 0, a2 = 0;
 #pragma unroll
-            for (int k = 0; k < F::CPL; ++k) {
-                s += chunk_dot<WT>(b.v[i][k], xr + k * F::CPC);
-                if constexpr (GLU) su += chunk_dot<WT>(b.vu[i][k], xr + k * F::CPC);
+                        for (int c = 0; c < 2; ++c)
+#pragma unroll
+                            for (int t = 0; t < 4; ++t) {
+                                const int w = static_cast<int>(v[c][t]);
+                                a0 = __builtin_amdgcn_sdot4(w, static_cast<int>(dg[(0 + c) * 4 + t]), a0, false);
+                                a1 = __builtin_amdgcn_sdot4(w, static_cast<int>(dg[(2 + c) * 4 + t]), a1, false);
+                                a2 = __builtin_amdgcn_sdot4(w, static_cast<int>(dg[(4 + c) * 4 + t]), a2, false);
+                            }
+                        return fmaf(fmaf(static_cast<float>(a2), 256.f, static_cast<float>(a1)), 256.f, static_cast<float>(a0));
+                    } else {
+                        int ac[6] = {0, 0, 0, 0, 0, 0};
+#pragma unroll
+                        for (int t = 0; t < 4; ++t) {
+                            const int w = static_cast<int>(v[0][t] ^ 0x88888888u);
+#pragma unroll
+                            for (int k = 0; k < 6; ++k) ac[k] = __builtin_amdgcn_sdot8(w, static_cast<int>(dg[4 * k + t]), ac[k], false);
+                        }
+                        const int p0 = ac[0] + 16 * ac[1], p1 = ac[2] + 16 * ac[3], p2 = ac[4] + 16 * ac[5];
+                        return fmaf(static_cast<float>(p2), 65536.f, static_cast<float>(p0 + 256 * p1)) * half_bits_to_float(g);
+                    }
+                };
+                d[i] = wave_sum(dot(b.v[i], b.g[i])) * dsc;
+                du[i] = 0.f;
+                if constexpr (GLU) du[i] = wave_sum(dot(b.vu[i], b.gu[i])) * dsc;
+            } else {
+                float s = 0.f, su = 0.f;
+#pragma unroll
+                for (int k = 0; k < F::CPL; ++k) {
+                    s += chunk_dot<WT>(b.v[i][k], xr + k * F::CPC);
+                    if constexpr (GLU) su += chunk_dot<WT>(b.vu[i][k], xr + k * F::CPC);
+                }
+                if constexpr (WT == WType::INT8) {
+                    s -= kBias<WT> * xsum;
+                    if constexpr (GLU) su -= kBias<WT> * xsum;
+                }
+                if constexpr (WT == WType::INT4) {
+                    s = half_bits_to_float(b.g[i]) * (s - 8.f * xsum);
+                    if constexpr (GLU) su = half_bits_to_float(b.gu[i]) * (su - 8.f * xsum);
+                }
+                d[i] = wave_sum(s);
+                du[i] = GLU ? wave_sum(su) : 0.f;
             }
-            if constexpr (WT == WType::INT8) {
-                s -= kBias<WT> * xsum;
-                if constexpr (GLU) su -= kBias<WT> * xsum;
-            }
-            if constexpr (WT == WType::INT4) {
-                s = half_bits_to_float(b.g[i]) * (s - 8.f * xsum);
-                if constexpr (GLU) su = half_bits_to_float(b.gu[i]) * (su - 8.f * xsum);
-            }
-            d[i] = wave_sum(s);
-            du[i] = GLU ? wave_sum(su) : 0.f;
         }
 
         // Lane i (< R) holds row r0 + i.
