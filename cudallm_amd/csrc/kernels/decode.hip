@@ -1149,6 +1149,10 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
     constexpr int NX = F::CPL * F::CPC;
     constexpr bool kDig = WT != WType::BF16;  // gate_up, down and lm_head use the integer dot products
     constexpr bool kQkvDig = WT == WType::INT8;  // and int8's qkv
+    // int4 writes the current token's fp16 KV cache rows from the attention workgroup that holds them (one 128-byte
+    // store per row) instead of 2-byte stores from 32 waves of the qkv phase: int4 -7 us per step on MI355X; bf16 +3
+    // and int8 +1 us, so they keep the qkv phase's stores.
+    constexpr bool kKvInAttn = WT == WType::INT4;
     __shared__ Smem<WT> sm;
 
     if (threadIdx.x < kCW) {
@@ -1316,7 +1320,7 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
                     }
                     tstore(tqkv + r0, o0, tg + T_QKV);
                     tstore(tqkv + r0 + 32, o1, tg + T_QKV);
-                    if (h >= NH) {
+                    if (!kKvInAttn && h >= NH) {
                         uint16_t* cache = h < NH + NKV ? p.k_cache : p.v_cache;
                         const size_t off = l * layer_cache + (static_cast<size_t>((h - NH) % NKV) * p.max_seq + pos) * HD;
                         *glob(cache + off + i) = float_to_half_bits(o0);
@@ -1378,11 +1382,18 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
                       qv, kv);
                 qs[tid] = qv;
                 if (cur) {
+                    // The current token's k (wave 0) and v (wave 1) into the tiles; for int4 also into the fp16 cache,
+                    // one 128-byte row per wave (the workgroup of the split holding pos is the one writer per kv head).
                     const int r = pos - t0;
+                    const uint16_t hb = float_to_half_bits(kv);
                     if (tid < HD) {
-                        Ks16[r * 2 * kKs + tid] = float_to_half_bits(kv);
+                        Ks16[r * 2 * kKs + tid] = hb;
+                        if constexpr (kKvInAttn)
+                            *glob(p.k_cache + l * layer_cache + (static_cast<size_t>(kvh) * p.max_seq + pos) * HD + tid) = hb;
                     } else {
-                        Vs16[r * HD + tid - HD] = float_to_half_bits(kv);
+                        Vs16[r * HD + tid - HD] = hb;
+                        if constexpr (kKvInAttn)
+                            *glob(p.v_cache + l * layer_cache + (static_cast<size_t>(kvh) * p.max_seq + pos) * HD + tid - HD) = hb;
                     }
                 }
                 stamp_attn(p, l, first, 1);
