@@ -438,8 +438,9 @@ __device__ __forceinline__ int swz(int i) {
 // With TWO, each thread first polls only its last entry and loads the others once that one is current: a wait
 // that starts long before the producers finish then keeps 1/PT of the polls in flight, which leaves the memory
 // path to the producers' stores.  Measured on MI355X for the wo input, which every workgroup starts polling while
-// the few attention workgroups still compute: int4 -16, int8 -4 us per step (bf16 +3, so bf16 keeps one stage),
-// and for int8's gate_up input a further -9 us.
+// the few attention workgroups still compute: int4 -16, int8 -4 us per step, and bf16 -4.6 us once attention wrote
+// whole lines (+3 before); for int8's gate_up input a further -9 us.  Polling one stage again (after the whole-line
+// attention stores): int8 +6, int4 +16 us.
 template <int N, bool SQ, int SWZ = 0, int MX = 0, bool TWO = false>
 __device__ __forceinline__ void fetch(const uint64_t* src, unsigned tag, float* dst, float* part, unsigned* err, int tid,
                       const float* g = nullptr, float* pmax = nullptr) {
@@ -1539,7 +1540,7 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
         {
             stall_at(p, kStallWo);
             if constexpr (!kDig) cwait(sm.bar, ep_in, lbad);  // every wave has read the qkv input (as above)
-            fetch<H, false, 0, 0, kDig>(tatt, tg + T_ATT, sm.big, sm.part, err, tid);
+            fetch<H, false, 0, 0, true>(tatt, tg + T_ATT, sm.big, sm.part, err, tid);
             cbar(sm.bar, ep, wave, lane, lbad);
             stamp_in(p, l, 3, 0);
             stall_at(p, kStallInputs);
