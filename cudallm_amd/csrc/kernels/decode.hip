@@ -946,7 +946,9 @@ __device__ __forceinline__ void down_dot2_dig8(Smem<WType::INT8>& sm, Cons& cs, 
 }
 
 // Per-chunk sums of the lane's down-projection inputs (the bias correction of quantised chunks);
-// the same for every row, so computed once per phase.
+// the same for every row, so computed once per phase.  The quantised down rows now use the digit
+// dots, so only bf16 (with nothing to sum) calls this; the unused variable stays in the quantised
+// kernels because deleting it changed int4's schedule of the merge phase (3 us per step slower).
 template <WType WT>
 struct DownSums {
     float v[RingCfg<WT>::kQuant ? RingCfg<WT>::LPR8 : 1];
