@@ -439,7 +439,7 @@ __device__ __forceinline__ int swz(int i) {
 // that starts long before the producers finish then keeps 1/PT of the polls in flight, which leaves the memory
 // path to the producers' stores.  Measured on MI355X for the wo input, which every workgroup starts polling while
 // the few attention workgroups still compute: int4 -16, int8 -4 us per step, and bf16 -4.6 us once attention wrote
-// whole lines (+3 before); for int8's gate_up input a further -9 us.  Polling one stage again (after the whole-line
+// whole lines (+3 before); for int8's gate_up input a further -9 us, and for int8's qkv input -2 us.  Polling one stage again (after the whole-line
 // attention stores): int8 +6, int4 +16 us.
 template <int N, bool SQ, int SWZ = 0, int MX = 0, bool TWO = false>
 __device__ __forceinline__ void fetch(const uint64_t* src, unsigned tag, float* dst, float* part, unsigned* err, int tid,
@@ -1271,7 +1271,7 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
                 const Norm8 gn = load_norm8(Lw.attn_norm, tid);
                 stall_at(p, kStallQkv);
                 if (l > 0) {
-                    fetch<H, true, 0, 1>(p.tx + static_cast<size_t>(l) * H, tg - kTagStride + T_X, sm.big + kXin<WT>,
+                    fetch<H, true, 0, 1, true>(p.tx + static_cast<size_t>(l) * H, tg - kTagStride + T_X, sm.big + kXin<WT>,
                                          sm.part, err, tid, Lw.attn_norm, sm.pmax);
                     cbar(sm.bar, ep, wave, lane, lbad);
                 }
