@@ -68,7 +68,7 @@ constexpr int kPairs = QKV / 2;          // RoPE pairs (i, i+32) of every q/k/v 
 #define CLLM_LM_ROWS_BF16 2
 #endif
 #ifndef CLLM_LM_ROWS_QUANT
-#define CLLM_LM_ROWS_QUANT 4
+#define CLLM_LM_ROWS_QUANT 8
 #endif
 template <WType WT>
 constexpr int kLmR = WT == WType::BF16 ? CLLM_LM_ROWS_BF16 : CLLM_LM_ROWS_QUANT;  // lm_head rows per unit

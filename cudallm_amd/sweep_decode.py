@@ -9,7 +9,7 @@ The knobs (compile-time constants of csrc/kernels/decode.hip):
   CLLM_RING_SLOTS_BF16   LDS ring slots per compute wave, bf16 weights            default 30 (the most that fits)
   CLLM_RING_SLOTS_QUANT  LDS ring slots per compute wave, int8 / int4 weights     default 22
   CLLM_LM_ROWS_BF16      lm_head rows per unit of work, bf16 weights               default 2
-  CLLM_LM_ROWS_QUANT     lm_head rows per unit of work, int8 / int4 weights        default 4
+  CLLM_LM_ROWS_QUANT     lm_head rows per unit of work, int8 / int4 weights        default 8
 ``build`` compiles one library per configuration (one knob moved from the default at a time) into OUT_DIR/NAME/;
 a configuration whose LDS does not fit fails to build and is reported as such.  ``run`` (on the GPU) times each
 library with bench.py's decode leg (CUDALLM_LIB selects the library) and reports the decode kernel's microseconds
@@ -25,10 +25,10 @@ from pathlib import Path
 PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 DEFAULTS = {"CLLM_LOADER_LINES": 16, "CLLM_RING_SLOTS_BF16": 30, "CLLM_RING_SLOTS_QUANT": 22, "CLLM_LM_ROWS_BF16": 2,
-            "CLLM_LM_ROWS_QUANT": 4}
+            "CLLM_LM_ROWS_QUANT": 8}
 # One knob at a time around the defaults.
 MOVES = {"CLLM_LOADER_LINES": (12, 20), "CLLM_RING_SLOTS_BF16": (26,), "CLLM_RING_SLOTS_QUANT": (20, 24),
-         "CLLM_LM_ROWS_BF16": (1, 4), "CLLM_LM_ROWS_QUANT": (2, 8)}
+         "CLLM_LM_ROWS_BF16": (1, 4), "CLLM_LM_ROWS_QUANT": (4, 16)}
 
 
 def configs() -> dict:

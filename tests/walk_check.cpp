@@ -6,7 +6,7 @@
 //   walk_check GRID [GRID ...]      prints "ok GRID" per grid that matches, or the first mismatch, and exits 1 on any
 //
 // The compute side below restates decode.hip's phase loops (u = gw, gw + NW, ... and their row formulas); lm_head
-// units of 1, 2 and 4 rows are checked (the kernel uses 2 for bf16 and 4 for int8/int4).
+// units of 1, 2, 4 and 8 rows are checked (the kernel uses 2 for bf16 and 8 for int8/int4).
 #include <cstdio>
 #include <cstdlib>
 #include <vector>
@@ -85,7 +85,7 @@ int main(int argc, char** argv) {
         for (WType wt : {WType::BF16, WType::INT8, WType::INT4})
             for (int s = 0; s < 5 && ok; ++s)
                 for (int gw : {0, 1, 31, 32, 33, NW / 2 + 5, NW - 33, NW - 1})
-                    for (int lm_rows : {1, 2, 4})
+                    for (int lm_rows : {1, 2, 4, 8})
                         if (ok && gw >= 0 && gw < NW) ok = check(wt, s, gw, NW, grid, lm_rows);
         if (ok) std::printf("ok %d\n", grid);
         bad += !ok;
