@@ -28,7 +28,7 @@ DEFAULTS = {"CLLM_LOADER_LINES": 16, "CLLM_RING_SLOTS_BF16": 30, "CLLM_RING_SLOT
             "CLLM_LM_ROWS_QUANT": 8}
 # One knob at a time around the defaults.
 MOVES = {"CLLM_LOADER_LINES": (12, 20), "CLLM_RING_SLOTS_BF16": (26,), "CLLM_RING_SLOTS_QUANT": (20, 24),
-         "CLLM_LM_ROWS_BF16": (1, 4), "CLLM_LM_ROWS_QUANT": (4, 16)}
+         "CLLM_LM_ROWS_BF16": (1, 4), "CLLM_LM_ROWS_QUANT": (2, 4)}
 
 
 def configs() -> dict:
