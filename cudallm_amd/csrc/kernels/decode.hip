@@ -1354,11 +1354,14 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
             constexpr int kTile = kAttnChunk * 8 / kCT;               // 16-byte chunks per thread
             const int T = NKV * nsplit;
             stall_at(p, kStallAttn);
+            // Tasks start at workgroup G / 2: the second half of the grid has one qkv unit per wave (the first half
+            // two), so its workgroups reach the attention phase sooner.
+            const int ab = (static_cast<int>(blockIdx.x) + G / 2) % G;
 #pragma unroll 1
-            for (int t = blockIdx.x; t < T; t += G) {
+            for (int t = ab; t < T; t += G) {
                 const int kvh = t % NKV, split = t / NKV;
                 const int t0 = split * kAttnChunk, n = min(kAttnChunk, ctx - t0);
-                const bool first = t == static_cast<int>(blockIdx.x);
+                const bool first = t == ab;
                 stamp_attn(p, l, first, 0);
                 const uint16_t* Kg = p.k_cache + l * layer_cache + static_cast<size_t>(kvh) * p.max_seq * HD;
                 const uint16_t* Vg = p.v_cache + l * layer_cache + static_cast<size_t>(kvh) * p.max_seq * HD;
