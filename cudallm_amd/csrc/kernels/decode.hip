@@ -117,9 +117,9 @@ struct RingCfg {
     static constexpr int NB = CLLM_LOADER_LINES;
 };
 
-// A compute wave takes every line of a unit (two 2048-wide rows; an lm_head unit of kLmR rows) before it releases
-// any, so a unit must fit its ring: otherwise the loader can never publish the unit's last lines and the wait for
-// them runs out (an error, not a result).
+// A compute wave waits for every line of a unit (two 2048-wide rows; an lm_head unit of kLmR rows) before it
+// releases any, so a unit must fit its ring: otherwise the loader can never publish the unit's last lines and the
+// wait for them runs out (an error, not a result).
 template <WType WT>
 constexpr bool kUnitsFitRing = 2 * RingCfg<WT>::LPR2 <= RingCfg<WT>::S && kLmR<WT> * RingCfg<WT>::LPR2 <= RingCfg<WT>::S;
 static_assert(kUnitsFitRing<WType::BF16> && kUnitsFitRing<WType::INT8> && kUnitsFitRing<WType::INT4>,
