@@ -1,4 +1,5 @@
-"""Batch-1 decode benchmark on one MI355X (kernel lines for configs 1-4).
+"""Batch-1 decode benchmark on one MI355X (the reference's headline run: 16-token prompt + 256 greedy
+tokens; kernel lines for its matvec and attention cases).
 
     python bench.py [--gpus 1] [--steps 256] [--warmup 16] [--dtypes bf16,int8,int4] [--no-cpu]
 
@@ -84,9 +85,10 @@ def bench_decode(path, wd: str, steps: int, warmup: int, torch) -> dict:
 
 
 def bench_config5(path, reps: int = 5, warmup: int = 1, prompt: int = PROMPT, gen: int = 256) -> dict:
-    """BASELINE config 5 timed the way reference src/tools/cudallm_bench.cpp:64-85 times it: per rep, reset, the
-    prompt, a drained stream, then `gen` greedy steps (token -1, no host sync) timed to the drained end; the median
-    tok/s over `reps` reps after `warmup` untimed reps.  Bytes per token = weight bytes + 32768 (prompt + ceil(gen/2))."""
+    """The headline run (16-token prompt, 256 greedy tokens) timed the way reference
+    src/tools/cudallm_bench.cpp:64-85 times it: per rep, reset, the prompt, a drained stream, then `gen` greedy
+    steps (token -1, no host sync) timed to the drained end; the median tok/s over `reps` reps after `warmup`
+    untimed reps.  Bytes per token = weight bytes + 32768 (prompt + ceil(gen/2))."""
     from cudallm_amd import engine as E
     ids = prompt_ids(prompt)
     rates = []
@@ -174,7 +176,7 @@ def host_description() -> dict:
 
 
 def cpu_matvec_config1(reps: int = 20) -> dict:
-    """BASELINE config 1 on the CPU: int8 8192x2048 dequantised to fp32 then W @ x (reference.py:33-37)."""
+    """The reference's int8 8192x2048 matvec case on the CPU: dequantised to fp32 then W @ x (reference.py:33-37)."""
     import torch
     from oracle import quantize as Q
     rng = np.random.default_rng(1)

@@ -2,8 +2,8 @@
 
 Follows the reference's tests/test_engine_vs_reference.py:10-94 (same option configurations and
 tolerances: residual rel-L2 < 1e-3, logits max |d| < 2e-2, argmax agreement, next == argmax,
-bit-identical re-run after reset) on seeded synthetic Llama-3.2-1B-shaped files
-instead of the HF checkpoint, plus graph-vs-eager identity, greedy decoding and state errors.
+bit-identical re-run after reset) on seeded synthetic Llama-3.2-1B-shaped files (the headline benchmark's
+model) instead of the HF checkpoint, plus graph-vs-eager identity, greedy decoding and state errors.
 """
 import os
 

@@ -1,8 +1,8 @@
 """GPU parity of every single-kernel hook against the oracle's float64 closed forms.
 
 Mirrors the reference's tests/test_kernels.py:43-229 (same seeds, shapes, grids and tolerances),
-then widens it: every Llama-3.2-1B projection shape (BASELINE config 2/3), the generic-width
-matvec path, context lengths up to 8192 (config 4), and the GPU quantisers bit-exact.
+then widens it: every Llama-3.2-1B projection shape the reference benchmarks, the generic-width
+matvec path, context lengths up to 8192 (its long-context attention case), and the GPU quantisers bit-exact.
 """
 import numpy as np
 import pytest
@@ -75,8 +75,8 @@ def test_matvec_opt(wtype, epilogue, fuse_norm, rpb, shape):
     _check_matvec(wtype, epilogue, fuse_norm, rpb, rows, cols, seed=20 + rows + cols)
 
 
-# BASELINE configs 2/3: every projection shape, engine epilogues (norm fused on the input side of
-# q/k/v/gate/up/lm_head, residual add on o/down), bf16-rounded N(0, 0.02) master weights.
+# Every projection shape the reference benchmarks, with the engine epilogues (norm fused on the input side
+# of q/k/v/gate/up/lm_head, residual add on o/down), bf16-rounded N(0, 0.02) master weights.
 MODEL_SHAPES = [("q", 2048, 2048, "store", 1), ("k", 512, 2048, "store", 1), ("v", 512, 2048, "store", 1),
                 ("o", 2048, 2048, "add", 0), ("gate", 8192, 2048, "store", 1), ("up", 8192, 2048, "store", 1),
                 ("down", 2048, 8192, "add", 0), ("wqkv", 3072, 2048, "store", 1),
@@ -100,7 +100,7 @@ def test_matvec_generic_and_ragged(wtype, rows, cols, epilogue):
 
 
 def test_matvec_config1_int8_known_case():
-    """int8 8192x2048, bf16 master N(0, 0.02), x bf16 N(0, 1), checked in float64."""
+    """The reference's int8 8192x2048 matvec case: bf16 master N(0, 0.02), x bf16 N(0, 1), checked in float64."""
     rng = np.random.default_rng(1)
     w = Q.bf16_bits_to_f32(Q.bf16_round_bits(rng.normal(0, 0.02, size=(8192, 2048)).astype(np.float32)))
     x = Q.bf16_bits_to_f32(Q.bf16_round_bits(rng.standard_normal(2048).astype(np.float32)))
@@ -173,7 +173,7 @@ def test_attention(impl, ctx, attn_data):
 
 @pytest.mark.parametrize("ctx", [128, 512, 2048, 4096, 8192, 8191])
 def test_attention_config4_long_context(ctx):
-    """max_seq 8192 (grid 8 x 64 splits), chunk 128, LSE merge."""
+    """The reference's long-context attention case: max_seq 8192 (grid 8 x 64 splits), chunk 128, LSE merge."""
     rng = np.random.default_rng(40 + ctx)
     q = rng.standard_normal(NH * HD).astype(np.float32)
     k = rng.standard_normal((NKV, 8192, HD)).astype(np.float16)

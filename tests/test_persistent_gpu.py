@@ -6,7 +6,7 @@
   wo + residual, gate_up with the RMSNorm prologue and SwiGLU, down + residual, lm_head with the final norm.
   This pins the persistent kernel's own row dots (fp32 FMA for bf16, biased-byte and integer-digit dots for
   int8/int4), not only the standalone matvec kernels the hooks run.
-* BASELINE config 5's whole sequence (16 prompt tokens + 256 greedy tokens) against the CPU oracle at the
+* The headline benchmark's whole sequence (16 prompt tokens + 256 greedy tokens) against the CPU oracle at the
   integration tolerances of the reference's tests/test_engine_vs_reference.py:62-94.
 * Timing perturbation, the epoch restart of the tagged words and contexts past 8192 against unperturbed runs
   or the multi-kernel path.
@@ -26,7 +26,7 @@ pytestmark = [pytest.mark.gpu, pytest.mark.timeout(900)]
 RTOL = ATOL = 1e-4          # reference tests/test_kernels.py:50,96 (matvec), :196 (attention)
 NH, NKV, HD, H, I = 32, 8, 64, 2048, 8192
 PROMPT = [128000] + [int(t) for t in np.random.default_rng(16).integers(0, 128256, 15)]
-SEQ_STEPS = 272             # config 5: 16 prompt + 256 generated positions
+SEQ_STEPS = 272             # the headline run: 16 prompt + 256 generated positions
 TRACE_CHECK_POS = (0, 1, 127, 128, 129, 255, 256, 257, 271)
 TRACE_CHECK_LAYERS = (0, 6, 15)
 
@@ -135,7 +135,7 @@ def test_phases_match_float64(wd, model_path):
 
 @pytest.mark.parametrize("wd", ["bf16", "int8", "int4"])
 def test_config5_sequence_matches_oracle(wd, model_path):
-    """a 16-token prompt and the oracle's own 256 greedy tokens, teacher-forced through the
+    """The headline run: a 16-token prompt and the oracle's own 256 greedy tokens, teacher-forced through the
     persistent kernel.  Logits within 2e-2 at every position, the engine's argmax equal to the oracle's token
     except at near-ties (oracle margin < 2e-2), and the residual stream within rel-L2 1e-3 at the split
     boundaries (reference tests/test_engine_vs_reference.py:62-94)."""
