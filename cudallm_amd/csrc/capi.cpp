@@ -238,6 +238,17 @@ int cudallm_get_stream(cudallm_engine* e, void** stream_out) {
     });
 }
 
+int cudallm_get_step_kind(cudallm_engine* e, int* kind_out, int* grid_out) {
+    if (kind_out) *kind_out = -1;
+    if (grid_out) *grid_out = 0;
+    return abi_entry("cudallm_get_step_kind", [&] {
+        cllm::Engine& eng = engine_of(e);
+        need(kind_out && grid_out, "kind_out and grid_out are required");
+        *kind_out = eng.persistent() ? 1 : 0;
+        *grid_out = eng.persistent() ? eng.grid() : 0;
+    });
+}
+
 int cudallm_kernel_matvec(int impl, int weight_dtype, int epilogue, int fuse_norm, int rpb, const void* w,
                           unsigned long long w_bytes, const void* scales, unsigned long long scales_bytes,
                           const float* x, const float* norm_w, float eps, float* y, int rows, int cols) {

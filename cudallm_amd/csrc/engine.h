@@ -52,6 +52,7 @@ public:
     uint64_t weight_bytes() const { return weights_->weight_bytes(); }
     int pos() const { return host_pos_; }
     bool persistent() const { return persistent_; }
+    int grid() const { return grid_; }
     hipStream_t stream() const { return stream_; }
 
     void reset();

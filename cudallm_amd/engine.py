@@ -63,6 +63,7 @@ SIGNATURES = {
     "cudallm_step_profile": ([c_void_p, c_int, POINTER(c_ulonglong), c_longlong, _I32P], c_int),
     "cudallm_step_trace": ([c_void_p, c_int, _F32P, c_longlong, _F32P, _I32P], c_int),
     "cudallm_get_stream": ([c_void_p, POINTER(c_void_p)], c_int),
+    "cudallm_get_step_kind": ([c_void_p, _I32P, _I32P], c_int),
     "cudallm_kernel_matvec": ([c_int, c_int, c_int, c_int, c_int, c_void_p, c_ulonglong, c_void_p, c_ulonglong,
                                _F32P, _F32P, c_float, _F32P, c_int, c_int], c_int),
     "cudallm_kernel_rmsnorm": ([_F32P, _F32P, c_float, _F32P, c_int], c_int),
@@ -188,6 +189,18 @@ class Engine:
         s = c_void_p()
         call("cudallm_get_stream", self.handle, ctypes.byref(s))
         return s.value or 0
+
+    @property
+    def step_kind(self) -> tuple[str, int]:
+        """("persistent", grid) when each step is one launch of the persistent decode kernel, ("program", 0)
+        for the multi-kernel step."""
+        kind, grid = c_int(), c_int()
+        call("cudallm_get_step_kind", self.handle, ctypes.byref(kind), ctypes.byref(grid))
+        return ("persistent" if kind.value == 1 else "program"), grid.value
+
+    @property
+    def persistent(self) -> bool:
+        return self.step_kind[0] == "persistent"
 
     def reset(self) -> None:
         call("cudallm_reset", self.handle)

@@ -102,6 +102,12 @@ int  cudallm_step_trace(cudallm_engine* e, int token, float* trace_out, long lon
  * on this stream.  The stream belongs to the engine and dies with it. */
 int  cudallm_get_stream(cudallm_engine* e, void** stream_out);
 
+/* How this engine runs a step: *kind_out = 1 for the persistent decode kernel (one launch per token), 0 for the
+ * multi-kernel program (the reference's ablation options, or a device where the persistent grid was not resident
+ * at once); *grid_out = the persistent kernel's workgroups (0 for the program).  No reference counterpart (the
+ * reference has one step path): benchmarks use it to refuse a run that did not time the kernel they name. */
+int  cudallm_get_step_kind(cudallm_engine* e, int* kind_out, int* grid_out);
+
 /* ---- single-kernel test hooks: host pointers in/out; allocate, copy, run, copy back, free ----
  * Reference cudallm.h:44-56 / cudallm_capi.cpp:179-316. */
 

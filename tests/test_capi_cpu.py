@@ -66,6 +66,9 @@ def test_null_arguments(lib):
     assert lib.cudallm_get_config(None, None) == INVALID_ARG
     s = ctypes.c_void_p(0)
     assert lib.cudallm_get_stream(None, ctypes.byref(s)) == INVALID_ARG and s.value is None
+    kind, grid = ctypes.c_int(7), ctypes.c_int(7)
+    assert lib.cudallm_get_step_kind(None, ctypes.byref(kind), ctypes.byref(grid)) == INVALID_ARG
+    assert kind.value == -1 and grid.value == 0
     lib.cudallm_destroy(None)
 
 
