@@ -5,10 +5,13 @@ tokens; kernel lines for its matvec and attention cases).
 
 A "step" is one batch-1 decode step (one token) of a seeded random-init Llama-3.2-1B-shaped model:
 16 layers, hidden 2048, FFN 8192, vocab 128256, GQA 32/8, tied embeddings, weights N(0, 0.02)
-(bf16 master; int8 per-row and int4 group-128 files quantised from it).  Per weight type: a 16-token
-seeded prompt, W untimed warm-up decode steps, then K greedy decode steps timed with the device
-drained on both sides; each step is one launch of the persistent decode kernel with the token fed
-back on the device (no host sync inside the timed region, as reference src/tools/cudallm_bench.cpp:64-80).
+(bf16 master; int8 per-row and int4 group-128 files quantised from it).  Per weight type: W untimed
+warm-up steps on a sequence of their own, then a reset, the 16-token seeded prompt, and K greedy decode
+steps timed with the device drained on both sides (positions 17 .. 16 + K: with K = 256 this is BASELINE's
+full-decode configuration, 16-token prompt + 256 greedy tokens); each step is one launch of the persistent
+decode kernel with the token fed back on the device (no host sync inside the timed region, as reference
+src/tools/cudallm_bench.cpp:64-80).  The run fails (exit 3) if an engine is not running the persistent kernel,
+so a line never names a kernel that did not run.
 
 Printed last, on one line: the JSON record.  ``value`` is bf16 decode tok/s; ``decode`` holds all
 three weight types; ``roofline`` is the dominant kernel, the persistent decode kernel (one launch
@@ -49,18 +52,29 @@ def prompt_ids(n: int) -> list[int]:
     return [128000] + [int(t) for t in rng.integers(0, 128256, n - 1)]
 
 
+class NotPersistent(RuntimeError):
+    """An engine ran the multi-kernel step where the benchmark times the persistent decode kernel."""
+
+
 def bench_decode(path, wd: str, steps: int, warmup: int, torch) -> dict:
     from cudallm_amd import engine as E
     t_load = time.perf_counter()
     with E.Engine(path) as eng:
         load_s = time.perf_counter() - t_load
+        kind, grid = eng.step_kind
+        if kind != "persistent":
+            raise NotPersistent(f"{wd}: the engine runs the multi-kernel step, not decode_kernel<{wd}>")
         weight_bytes = eng.config["weight_bytes"]
         ids = prompt_ids(PROMPT)
-        eng.reset()
+        eng.reset()  # warm-up on a sequence of its own
         for t in ids:
             eng.step_async(t)
         for _ in range(warmup):
             eng.step_async(None)
+        eng.reset()  # then the timed sequence: the prompt, and `steps` greedy steps from position 17 on
+        for t in ids[:-1]:
+            eng.step_async(t)
+        eng.step(ids[-1])  # the last prompt step returns its output: the stream is drained here
         torch.cuda.synchronize()
         # HIP events on the engine's own stream, where each step is one launch of the decode kernel.
         es = torch.cuda.ExternalStream(eng.stream)
@@ -74,14 +88,15 @@ def bench_decode(path, wd: str, steps: int, warmup: int, torch) -> dict:
         dt = time.perf_counter() - t0
         ev_us = ev0.elapsed_time(ev1) * 1e3 / steps
         nxt, _ = eng.step(None)
-    ctx0 = PROMPT + warmup
-    kv = KV_BYTES_PER_POS * (ctx0 + (steps + 1) // 2)  # reference cudallm_bench.cpp:82-85 accounting
+    ctx0 = PROMPT + 1  # the first timed step attends over 17 positions
+    kv = KV_BYTES_PER_POS * (PROMPT + (steps + 1) // 2)  # reference cudallm_bench.cpp:82-85 accounting
     bpt = weight_bytes + kv
     tok_s = steps / dt
     return {"tok_s": tok_s, "ms_per_token": 1e3 * dt / steps, "weight_bytes": weight_bytes, "bytes_per_token": bpt,
             "gbps": bpt * tok_s / 1e9, "frac_of_8tbs": bpt * tok_s / PEAK_HBM,
-            "roofline_tok_s": PEAK_HBM / bpt, "context": [ctx0, ctx0 + steps], "load_s": round(load_s, 2),
-            "last_token": nxt, "kernel_avg_us": ev_us, "kernel_gbps": bpt / ev_us / 1e3}
+            "roofline_tok_s": PEAK_HBM / bpt, "context": [ctx0, ctx0 + steps - 1], "load_s": round(load_s, 2),
+            "last_token": nxt, "kernel_avg_us": ev_us, "kernel_gbps": bpt / ev_us / 1e3,
+            "step_kind": kind, "grid": grid}
 
 
 def bench_config5(path, reps: int = 5, warmup: int = 1, prompt: int = PROMPT, gen: int = 256) -> dict:
@@ -93,6 +108,8 @@ def bench_config5(path, reps: int = 5, warmup: int = 1, prompt: int = PROMPT, ge
     ids = prompt_ids(prompt)
     rates = []
     with E.Engine(path, max_seq_len=4096) as eng:
+        if not eng.persistent:
+            raise NotPersistent("config 5: the engine runs the multi-kernel step, not the persistent kernel")
         weight_bytes = eng.config["weight_bytes"]
         for r in range(warmup + reps):
             eng.reset()
@@ -213,8 +230,8 @@ def main() -> int:
         print("bench.py: this build measures one GPU only (batch-1 decode does not shard across GPUs here); "
               "run it with --gpus 1", file=sys.stderr)
         return 2
-    if PROMPT + args.warmup + args.steps + 1 > 4096:
-        print("bench.py: prompt + warmup + steps must fit the 4096-token context", file=sys.stderr)
+    if PROMPT + max(args.warmup, args.steps) + 1 > 4096:
+        print("bench.py: prompt + warmup and prompt + steps must fit the 4096-token context", file=sys.stderr)
         return 2
 
     import torch
@@ -243,12 +260,20 @@ def main() -> int:
         t0 = time.perf_counter()
         synth.write_model(paths[wd], wd, seed=1234)
         log(f"[bench] wrote {wd} model in {time.perf_counter() - t0:.1f} s")
-        decode[wd] = bench_decode(paths[wd], wd, args.steps, args.warmup, torch)
+        try:
+            decode[wd] = bench_decode(paths[wd], wd, args.steps, args.warmup, torch)
+        except NotPersistent as e:
+            print(f"bench.py: {e}; refusing to report it as the persistent kernel's line", file=sys.stderr)
+            return 3
         log(f"[bench] decode {wd}: {decode[wd]['tok_s']:.1f} tok/s, {decode[wd]['gbps']:.0f} GB/s "
             f"({100 * decode[wd]['frac_of_8tbs']:.1f} % of 8 TB/s); kernel {decode[wd]['kernel_avg_us']:.1f} us "
             f"by events")
         if not args.no_config5:
-            decode[wd]["config5"] = bench_config5(paths[wd])
+            try:
+                decode[wd]["config5"] = bench_config5(paths[wd])
+            except NotPersistent as e:
+                print(f"bench.py: {e}", file=sys.stderr)
+                return 3
             c5 = decode[wd]["config5"]
             log(f"[bench] config 5 {wd} (16 + 256, median of {c5['reps']}): {c5['tok_s']:.1f} tok/s, "
                 f"{100 * c5['frac_of_8tbs']:.1f} % of 8 TB/s")
@@ -295,10 +320,14 @@ def main() -> int:
         "warmup": args.warmup, "ms_per_step": round(head["ms_per_token"], 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": head_wd,
         "data": "synthetic: seeded random-init Llama-3.2-1B-shaped weights N(0,0.02), bf16 master",
-        "config": {"workload": f"batch-1 greedy decode, {head_wd} weights, 16-token prompt + {args.warmup} warm-up "
-                               f"+ {args.steps} timed steps, one kernel launch per step (BASELINE config 5)",
+        "config": {"workload": f"batch-1 greedy decode, {head_wd} weights: 16-token prompt, then {args.steps} timed "
+                               f"greedy steps at contexts {head['context'][0]}..{head['context'][1]}, one kernel "
+                               f"launch per step ({args.warmup} warm-up steps on a separate sequence)"
+                               + (" = BASELINE's full-decode configuration" if args.steps == 256 else
+                                  "; BASELINE's full-decode configuration (256 steps) is decode.*.config5"),
                    "model": "llama-3.2-1b-shaped (random init)", "global_batch": 1,
-                   "seq_len": PROMPT + args.warmup + args.steps, "parallelism": "none (1 GPU)"},
+                   "seq_len": PROMPT + args.steps, "parallelism": "none (1 GPU)",
+                   "step_kind": f"{head['step_kind']} (grid {head['grid']})"},
         "roofline": {"bound": "hbm", "achieved": round(head["kernel_gbps"], 1), "peak": 8000.0, "unit": "GB/s",
                      "frac": round(head["kernel_gbps"] / 8000.0, 4), "traffic": traffic_bytes(f"decode_kernel<{head_wd}>"),
                      "kernel": f"decode_kernel<{head_wd}> (persistent: the whole decode step is this one launch)",
