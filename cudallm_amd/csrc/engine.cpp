@@ -122,7 +122,14 @@ Engine::Engine(const std::string& path, const EngineOptions& opts) : opts_(opts)
         // CUDALLM_PERSISTENT=0 selects the multi-kernel step instead (for comparisons).
         const char* env = std::getenv("CUDALLM_PERSISTENT");
         const bool wanted = opts_.fuse && opts_.matvec == 1 && opts_.attn == 1 && !(env && !std::strcmp(env, "0"));
+        // CUDALLM_DECODE_GRID overrides the grid (a multiple of 8, at most the CU count) for grid-size sweeps.
         grid_ = device_cu_count();
+        if (const char* g = std::getenv("CUDALLM_DECODE_GRID")) {
+            const int want = std::atoi(g);
+            CLLM_REQUIRE(want >= kDecodeMinGrid && want <= grid_ && want % 8 == 0,
+                         "CUDALLM_DECODE_GRID: a multiple of 8, at least 64 and at most the CU count");
+            grid_ = want;
+        }
         persistent_ = wanted && S <= static_cast<size_t>(kDecodeMaxSeq) && grid_ % 8 == 0 &&
                       grid_ >= kDecodeMinGrid && grid_ <= kDecodeMaxGrid && decode_max_grid(c.wt) >= grid_;
 

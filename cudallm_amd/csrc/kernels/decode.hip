@@ -933,20 +933,22 @@ __device__ __forceinline__ void down_dot2_dig4(Smem<WType::INT4>& sm, Cons& cs, 
 __device__ __forceinline__ void down_dot2_dig8(Smem<WType::INT8>& sm, Cons& cs, const uint32_t* tab, float sc, int wave,
                                                int lane, bool& lbad, float& d0, float& d1) {
     using C = RingCfg<WType::INT8>;
-    static_assert(C::LPR8 == 8 && C::S >= 16, "two int8 down rows fit the ring");
-    ring_wait(cs.k + 16, cs.cfull, &sm.full[wave], lbad);
+    constexpr int R = C::LPR8, HALF = R / 2;  // lines per row; each row is read in two halves of HALF lines
+    static_assert(R == 8 && C::S >= 2 * R, "two int8 down rows fit the ring");
+    ring_wait(cs.k + 2 * R, cs.cfull, &sm.full[wave], lbad);
     int a[2][3] = {{0, 0, 0}, {0, 0, 0}};
-    const float rs0 = ring_side<WType::INT8>(sm, cs, 0, wave, lane), rs1 = ring_side<WType::INT8>(sm, cs, 8, wave, lane);
+    const float rs0 = ring_side<WType::INT8>(sm, cs, 0, wave, lane), rs1 = ring_side<WType::INT8>(sm, cs, R, wave, lane);
 #pragma unroll
-    for (int c0 = 0; c0 < 8; c0 += 4) {
-        u32x4 w[2][4];
+    for (int c0 = 0; c0 < R; c0 += HALF) {
+        u32x4 w[2][HALF];
 #pragma unroll
-        for (int q = 0; q < 2; ++q) ring_read<WType::INT8, 4>(sm, cs, 8 * q + c0, wave, lane, w[q]);
-        // Release what has been read: after the first half the lines read form a prefix of 4 (lines 8..11 of the
-        // second row do not extend it), after the second half all 16 (int8 -2.7 us per step on MI355X).
-        if (lane == 0) lds_store(&sm.done[wave], cs.k + (c0 == 0 ? 4 : 16));
+        for (int q = 0; q < 2; ++q) ring_read<WType::INT8, HALF>(sm, cs, R * q + c0, wave, lane, w[q]);
+        // Release what has been read.  The ring holds row 0's R lines, then row 1's: after the first half the lines
+        // read form a prefix of HALF (row 1's first half does not extend it), after the second half all 2 R (int8
+        // -2.7 us per step on MI355X).
+        if (lane == 0) lds_store(&sm.done[wave], cs.k + (c0 == 0 ? HALF : 2 * R));
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
+        for (int g = 0; g < HALF; ++g) {
             const uint32_t* t = tab + ((c0 + g) * kWave + lane) * 4;
             const u32x4 e0 = *reinterpret_cast<const u32x4*>(t), e1 = *reinterpret_cast<const u32x4*>(t + 2 * kDownWords),
                         e2 = *reinterpret_cast<const u32x4*>(t + 4 * kDownWords);
@@ -961,7 +963,7 @@ __device__ __forceinline__ void down_dot2_dig8(Smem<WType::INT8>& sm, Cons& cs, 
                 }
         }
     }
-    ring_advance<WType::INT8>(cs, 16);
+    ring_advance<WType::INT8>(cs, 2 * R);
     const float t0 = fmaf(fmaf(static_cast<float>(a[0][2]), 256.f, static_cast<float>(a[0][1])), 256.f, static_cast<float>(a[0][0]));
     const float t1 = fmaf(fmaf(static_cast<float>(a[1][2]), 256.f, static_cast<float>(a[1][1])), 256.f, static_cast<float>(a[1][0]));
     d0 = wave_sum(t0) * sc * rs0;
@@ -1431,31 +1433,32 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
                 cbar(sm.bar, ep, wave, lane, lbad);
                 if (first) stamp_in(p, l, 1, 0);
                 stamp_attn(p, l, first, 2);
-                // wave w = query head kvh*4 + w; lane scores tokens lane and lane + 64.
+                // wave w = query head kvh*4 + w; lane scores tokens lane and lane + 64 together, 8 dimensions at a time:
+                // q's 8 values are read from LDS once per step (the same address in every lane) for both tokens, so q
+                // is never held whole in registers (64 VGPRs).  Rows past n are read (inside the tile) and replaced by
+                // -inf.
                 float s[2];
                 {
-                    f32x4 qv[HD / 4];
+                    float dd[2][4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-                    for (int i = 0; i < HD / 4; ++i) qv[i] = *reinterpret_cast<const f32x4*>(qs + wave * HD + 4 * i);
+                    for (int i = 0; i < HD / 8; ++i) {
+                        const f32x4 qa4 = *reinterpret_cast<const f32x4*>(qs + wave * HD + 8 * i);
+                        const f32x4 qb4 = *reinterpret_cast<const f32x4*>(qs + wave * HD + 8 * i + 4);
 #pragma unroll
-                    for (int k = 0; k < 2; ++k) {
-                        const int j = lane + kWave * k;
-                        if (j < n) {
-                            float dd[4] = {0.f, 0.f, 0.f, 0.f};
+                        for (int k = 0; k < 2; ++k) {
+                            const u32x4 kk = *reinterpret_cast<const u32x4*>(Ks + (lane + kWave * k) * kKs + 4 * i);
 #pragma unroll
-                            for (int i = 0; i < HD / 8; ++i) {
-                                const u32x4 kk = *reinterpret_cast<const u32x4*>(Ks + j * kKs + 4 * i);
-#pragma unroll
-                                for (int e = 0; e < 4; ++e) {
-                                    dd[e] = fmaf(half_bits_to_float(static_cast<uint16_t>(kk[e])), qv[2 * i + e / 2][2 * (e % 2)], dd[e]);
-                                    dd[e] = fmaf(half_bits_to_float(static_cast<uint16_t>(kk[e] >> 16)), qv[2 * i + e / 2][2 * (e % 2) + 1], dd[e]);
-                                }
+                            for (int e = 0; e < 4; ++e) {
+                                const float q0 = e < 2 ? qa4[2 * e] : qb4[2 * e - 4];
+                                const float q1 = e < 2 ? qa4[2 * e + 1] : qb4[2 * e - 3];
+                                dd[k][e] = fmaf(half_bits_to_float(static_cast<uint16_t>(kk[e])), q0, dd[k][e]);
+                                dd[k][e] = fmaf(half_bits_to_float(static_cast<uint16_t>(kk[e] >> 16)), q1, dd[k][e]);
                             }
-                            s[k] = 0.125f * ((dd[0] + dd[1]) + (dd[2] + dd[3]));  // 4 chains: 2.5-5.5 us per step
-                        } else {
-                            s[k] = -INFINITY;
                         }
                     }
+#pragma unroll
+                    for (int k = 0; k < 2; ++k)  // 4 chains per token: 2.5-5.5 us per step against one
+                        s[k] = lane + kWave * k < n ? 0.125f * ((dd[k][0] + dd[k][1]) + (dd[k][2] + dd[k][3])) : -INFINITY;
                 }
                 const float m = wave_max(fmaxf(s[0], s[1]));
                 const float p0 = lane < n ? expf(s[0] - m) : 0.f;

@@ -44,3 +44,36 @@ def test_units_that_do_not_fit_the_ring_are_refused(defines, message):
     r = front_end(defines)
     assert r.returncode != 0
     assert message in r.stderr, r.stderr[-2000:]
+
+
+def makefile_decode_command(obj: Path) -> list[str]:
+    """The Makefile's own compile command for the decode kernel (make -n), writing `obj`."""
+    r = subprocess.run(["make", "-n", "-B", "-C", str(ROOT / "cudallm_amd"), f"BUILD={obj.parent}", str(obj)],
+                       capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0, r.stderr
+    line = next(ln for ln in r.stdout.splitlines() if "decode.hip" in ln and "hipcc" in ln)
+    return line.split()
+
+
+def test_decode_kernels_use_no_scratch(tmp_path):
+    """The decode kernel, built exactly as the Makefile builds it, must keep every value in registers: no VGPR
+    spills and no scratch memory for any weight type.  The one build that miscomputed int4 results (layer 1's SwiGLU
+    outputs wrong in every workgroup, varying from run to run, cause not found) was the only one that spilled, and
+    the kernel sits at 252-254 of its 256 VGPRs, so a change that tips it into spills must fail here first."""
+    cmd = makefile_decode_command(tmp_path / "decode.o") + ["-Rpass-analysis=kernel-resource-usage"]
+    r = subprocess.run(cmd, capture_output=True, text=True, timeout=600, cwd=ROOT / "cudallm_amd")
+    assert r.returncode == 0, r.stderr[-2000:]
+    kernels = {}
+    name = None
+    for ln in r.stderr.splitlines():
+        if "Function Name:" in ln:
+            name = ln.split("Function Name:")[1].split()[0]
+        elif name and "remark:" in ln:
+            key, _, val = ln.split("remark:")[1].strip().partition(":")
+            kernels.setdefault(name, {})[key.strip()] = val.split("[")[0].strip()
+    decode = {k: v for k, v in kernels.items() if "decode_kernel" in k}
+    assert len(decode) == 3, sorted(kernels)
+    for k, v in decode.items():
+        assert v["ScratchSize [bytes/lane]"] == "0", (k, v)
+        assert v["VGPRs Spill"] == "0", (k, v)
+        assert int(v["VGPRs"]) <= 256, (k, v)

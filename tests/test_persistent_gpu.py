@@ -8,8 +8,10 @@
   int8/int4), not only the standalone matvec kernels the hooks run.
 * The headline benchmark's whole sequence (16 prompt tokens + 256 greedy tokens) against the CPU oracle at the
   integration tolerances of the reference's tests/test_engine_vs_reference.py:62-94.
-* Timing perturbation, the epoch restart of the tagged words and contexts past 8192 against unperturbed runs
-  or the multi-kernel path.
+* Timing perturbation, the epoch restart of the tagged words, contexts past 8192 and the largest max_seq_len
+  against unperturbed runs or the multi-kernel path, for every weight type.
+Every engine these tests time or trace is checked to run the persistent kernel (cudallm_get_step_kind), so a
+device where its grid was not resident cannot pass them on the multi-kernel step.
 """
 import os
 
@@ -64,6 +66,12 @@ class _Weights:
         return (q.reshape(q.shape[0], g.shape[1], -1) * g[:, :, None]).reshape(q.shape[0], -1)
 
 
+def _persistent(eng):
+    kind, grid = eng.step_kind
+    assert kind == "persistent" and grid > 0, f"the engine runs the {kind} step, not the persistent kernel"
+    return eng
+
+
 def _close(name, got, want):
     got = np.asarray(got, dtype=np.float64)
     err = np.abs(got - want) - (ATOL + RTOL * np.abs(want))
@@ -85,6 +93,7 @@ def test_phases_match_float64(wd, model_path):
     kv = {l: (np.zeros((NKV, SEQ_STEPS, HD), np.float16), np.zeros((NKV, SEQ_STEPS, HD), np.float16))
           for l in TRACE_CHECK_LAYERS}
     with E.Engine(path, max_seq_len=4096) as eng:
+        _persistent(eng)
         tok = PROMPT[0]
         for p in range(SEQ_STEPS):
             nxt, lg, tr = eng.step_trace(PROMPT[p] if p < len(PROMPT) else None)
@@ -153,6 +162,7 @@ def test_config5_sequence_matches_oracle(wd, model_path):
     del m
     worst_lg, worst_res, ties = 0.0, 0.0, []
     with E.Engine(path, max_seq_len=4096) as eng:
+        _persistent(eng)
         for p in range(SEQ_STEPS):
             if p in check_res:
                 nxt, lg, res = eng.step_debug(toks[p])
@@ -192,6 +202,7 @@ def test_stalls_across_splits_bit_identical(wd, model_path, monkeypatch):
     def run():
         out = []
         with E.Engine(model_path(wd), max_seq_len=256) as eng:
+            _persistent(eng)
             for p, t in enumerate(toks):
                 if p >= 126:
                     _, lg, res = eng.step_debug(t)
@@ -213,7 +224,7 @@ def test_stalls_across_splits_bit_identical(wd, model_path, monkeypatch):
         print(f"[stalls {wd}] {name} ({mask:#x}): bit-identical over positions 126..{steps - 1}", flush=True)
 
 
-@pytest.mark.parametrize("wd", ["bf16", "int4"])
+@pytest.mark.parametrize("wd", ["bf16", "int8", "int4"])
 def test_epoch_restart_is_bit_identical(wd, model_path, monkeypatch):
     """The host restarts the tag epochs (clears every tagged word, step counter back to 0) before the 32-bit tags
     could repeat; CUDALLM_EPOCH_LIMIT brings that point down to every 50 launches.  200 positions (2 splits, 3
@@ -223,6 +234,7 @@ def test_epoch_restart_is_bit_identical(wd, model_path, monkeypatch):
     def run():
         lgs = []
         with E.Engine(model_path(wd), max_seq_len=256) as eng:
+            _persistent(eng)
             for t in toks[:30]:
                 eng.step_async(t)
             eng.reset()
@@ -242,15 +254,19 @@ def test_epoch_restart_is_bit_identical(wd, model_path, monkeypatch):
     np.testing.assert_array_equal(got, base)
 
 
-def test_context_past_8192_matches_multikernel(model_path, monkeypatch):
+@pytest.mark.parametrize("wd", ["bf16", "int8", "int4"])
+def test_context_past_8192_matches_multikernel(wd, model_path, monkeypatch):
     """max_seq_len 16384 on the persistent kernel (more than 64 splits: the merge loops over 64-split blocks)
-    against the multi-kernel path, teacher-forced to position 9000 with int4 weights."""
+    against the multi-kernel path, teacher-forced to position 9000.  int4 writes the current token's KV rows from
+    the attention workgroup, bf16 and int8 from the qkv phase: both writers are covered past 8192 positions."""
     steps = 9000
     monkeypatch.setenv("CUDALLM_PERSISTENT", "0")
-    ref = E.Engine(model_path("int4"), max_seq_len=16384)
+    ref = E.Engine(model_path(wd), max_seq_len=16384)
     monkeypatch.delenv("CUDALLM_PERSISTENT")
-    eng = E.Engine(model_path("int4"), max_seq_len=16384)
+    eng = E.Engine(model_path(wd), max_seq_len=16384)
     try:
+        assert ref.step_kind[0] == "program"
+        _persistent(eng)
         toks, worst, agree, checked = [128000], 0.0, 0, 0
         for i in range(steps):
             check = i in (8190, 8191, 8192, 8193, 8319, 8320, 8999)
@@ -261,9 +277,43 @@ def test_context_past_8192_matches_multikernel(model_path, monkeypatch):
                 agree += int(n_eng == n_ref)
                 checked += 1
             toks.append(n_ref)
-        print(f"[engine] int4 persistent vs multi-kernel to ctx {steps}: worst rel logit diff {worst:.2e}, "
+        print(f"[engine] {wd} persistent vs multi-kernel to ctx {steps}: worst rel logit diff {worst:.2e}, "
               f"argmax agree {agree}/{checked}", flush=True)
         assert worst < 2e-3 and agree >= checked - 1
+    finally:
+        eng.close()
+        ref.close()
+
+
+@pytest.mark.parametrize("wd", ["bf16", "int8", "int4"])
+def test_largest_max_seq_matches_multikernel(wd, model_dir, gpu):
+    """max_seq_len 131072 (Llama-3.2's context, the kernel's largest: 1024 split slots per head, 4.3 GB of KV cache)
+    against the multi-kernel path over 300 positions (three splits): every stride that grows with max_seq_len (the
+    layer's KV cache, the split partials) at its largest value.  Contexts past 64 splits are the test above."""
+    from cudallm_amd import synth
+    path = model_dir / f"synth_seed7_{wd}_ms131072.cudallm"
+    if not path.exists():
+        synth.write_model(path, wd, seed=7, max_seq_len=131072)
+    os.environ["CUDALLM_PERSISTENT"] = "0"
+    try:
+        ref = E.Engine(path)
+    finally:
+        del os.environ["CUDALLM_PERSISTENT"]
+    eng = E.Engine(path)
+    try:
+        assert ref.step_kind[0] == "program" and eng.config["max_seq_len"] == 131072
+        _persistent(eng)
+        toks, worst = [128000], 0.0
+        for i in range(300):
+            check = i in (0, 127, 128, 255, 256, 299)
+            n_ref, lg_ref = ref.step(toks[-1], want_logits=check)
+            n_eng, lg_eng = eng.step(toks[-1], want_logits=check)
+            if check:
+                worst = max(worst, float(np.abs(lg_eng - lg_ref).max()) / float(np.abs(lg_ref).max()))
+                assert n_eng == n_ref or np.sort(lg_ref)[-2] > np.max(lg_ref) - 1e-3, f"argmax differs at {i}"
+            toks.append(n_ref)
+        print(f"[engine] {wd} max_seq 131072, 300 positions: worst rel logit diff {worst:.2e}", flush=True)
+        assert worst < 2e-3
     finally:
         eng.close()
         ref.close()

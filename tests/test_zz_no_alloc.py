@@ -56,3 +56,35 @@ def test_static_attention_rejects_more_than_its_slots(gpu):
         E.launch_attention_static(q.data_ptr(), kc.data_ptr(), vc.data_ptr(), pos.data_ptr(), q.data_ptr(), 32, 8, 64,
                                   288 * 128, None)
     assert ei.value.code == 1 and "8192" in str(ei.value)
+
+
+def test_static_attention_replays_under_graph_capture_and_allocates_nothing(gpu):
+    """The header's two claims: the call works under HIP graph capture (captured once after a warm-up call, replayed
+    three times with eager work and synchronisations in between, every replay equal to the workspace result), and
+    direct calls allocate nothing (device free memory unchanged across them)."""
+    import torch
+    rng = np.random.default_rng(5)
+    nh, nkv, max_seq, ctx = 32, 8, 1024, 700
+    q, kc, vc, pos = _case(torch, rng, nh, nkv, max_seq, ctx)
+    _, want = _run_both(torch, q, kc, vc, pos, nh, nkv, max_seq)  # also the warm-up call on this device
+    out = torch.full((nh * 64,), float("nan"), dtype=torch.float32, device="cuda")
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        E.launch_attention_static(q.data_ptr(), kc.data_ptr(), vc.data_ptr(), pos.data_ptr(), out.data_ptr(), nh, nkv,
+                                  64, max_seq, torch.cuda.current_stream().cuda_stream)
+    for rep in range(3):
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(out.cpu().numpy(), want, err_msg=f"graph replay {rep}")
+    del g
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info()[0]
+    s = torch.cuda.current_stream().cuda_stream
+    for _ in range(4):
+        E.launch_attention_static(q.data_ptr(), kc.data_ptr(), vc.data_ptr(), pos.data_ptr(), out.data_ptr(), nh, nkv,
+                                  64, max_seq, s)
+    torch.cuda.synchronize()
+    assert torch.cuda.mem_get_info()[0] == free0
+    np.testing.assert_array_equal(out.cpu().numpy(), want)
