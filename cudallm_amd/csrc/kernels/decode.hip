@@ -1433,32 +1433,31 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
                 cbar(sm.bar, ep, wave, lane, lbad);
                 if (first) stamp_in(p, l, 1, 0);
                 stamp_attn(p, l, first, 2);
-                // wave w = query head kvh*4 + w; lane scores tokens lane and lane + 64 together, 8 dimensions at a time:
-                // q's 8 values are read from LDS once per step (the same address in every lane) for both tokens, so q
-                // is never held whole in registers (64 VGPRs).  Rows past n are read (inside the tile) and replaced by
-                // -inf.
+                // wave w = query head kvh*4 + w; lane scores tokens lane and lane + 64.
                 float s[2];
                 {
-                    float dd[2][4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+                    f32x4 qv[HD / 4];
 #pragma unroll
-                    for (int i = 0; i < HD / 8; ++i) {
-                        const f32x4 qa4 = *reinterpret_cast<const f32x4*>(qs + wave * HD + 8 * i);
-                        const f32x4 qb4 = *reinterpret_cast<const f32x4*>(qs + wave * HD + 8 * i + 4);
+                    for (int i = 0; i < HD / 4; ++i) qv[i] = *reinterpret_cast<const f32x4*>(qs + wave * HD + 4 * i);
 #pragma unroll
-                        for (int k = 0; k < 2; ++k) {
-                            const u32x4 kk = *reinterpret_cast<const u32x4*>(Ks + (lane + kWave * k) * kKs + 4 * i);
+                    for (int k = 0; k < 2; ++k) {
+                        const int j = lane + kWave * k;
+                        if (j < n) {
+                            float dd[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                            for (int e = 0; e < 4; ++e) {
-                                const float q0 = e < 2 ? qa4[2 * e] : qb4[2 * e - 4];
-                                const float q1 = e < 2 ? qa4[2 * e + 1] : qb4[2 * e - 3];
-                                dd[k][e] = fmaf(half_bits_to_float(static_cast<uint16_t>(kk[e])), q0, dd[k][e]);
-                                dd[k][e] = fmaf(half_bits_to_float(static_cast<uint16_t>(kk[e] >> 16)), q1, dd[k][e]);
+                            for (int i = 0; i < HD / 8; ++i) {
+                                const u32x4 kk = *reinterpret_cast<const u32x4*>(Ks + j * kKs + 4 * i);
+#pragma unroll
+                                for (int e = 0; e < 4; ++e) {
+                                    dd[e] = fmaf(half_bits_to_float(static_cast<uint16_t>(kk[e])), qv[2 * i + e / 2][2 * (e % 2)], dd[e]);
+                                    dd[e] = fmaf(half_bits_to_float(static_cast<uint16_t>(kk[e] >> 16)), qv[2 * i + e / 2][2 * (e % 2) + 1], dd[e]);
+                                }
                             }
+                            s[k] = 0.125f * ((dd[0] + dd[1]) + (dd[2] + dd[3]));  // 4 chains: 2.5-5.5 us per step
+                        } else {
+                            s[k] = -INFINITY;
                         }
                     }
-#pragma unroll
-                    for (int k = 0; k < 2; ++k)  // 4 chains per token: 2.5-5.5 us per step against one
-                        s[k] = lane + kWave * k < n ? 0.125f * ((dd[k][0] + dd[k][1]) + (dd[k][2] + dd[k][3])) : -INFINITY;
                 }
                 const float m = wave_max(fmaxf(s[0], s[1]));
                 const float p0 = lane < n ? expf(s[0] - m) : 0.f;

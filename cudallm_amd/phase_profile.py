@@ -36,6 +36,9 @@ def profile(path, ctx: int, reps: int):
     return stamps
 
 
+ATTN_SLOT = 112  # kAttnSteps in decode.hip
+
+
 def summarise(wd: str, S: np.ndarray, ctx: int) -> list[str]:
     G = S.shape[0]
     rel = (S - S[:, 0].min()) / 100.0  # microseconds
@@ -77,6 +80,18 @@ def summarise(wd: str, S: np.ndarray, ctx: int) -> list[str]:
         lines.append(f"| {p} | {inp} | {pro} | +{med - pe:.2f} | {np.percentile(e, 10) - med:+.2f} | "
                      f"{e.max() - med:+.2f} |")
         pe = med
+    # Inside the first attention task of layer 1 (the workgroups that run one): when it started (K/V tile loads
+    # issued), had q (and the current k, v), passed its barrier, had the scores, had stored its output, and left.
+    steps = ["task start", "q, k, v arrived", "barrier passed", "scores, softmax", "output stored", "task end"]
+    att = S[:, ATTN_SLOT:ATTN_SLOT + len(steps)]
+    who = np.all(att > 0, axis=1)
+    if who.any():
+        qkv_end = np.median(rel[:, 7])
+        lines += ["", f"Layer 1's first attention task ({int(who.sum())} workgroups), us after qkv's median end:", "",
+                  "| step | median | max |", "|---|---|---|"]
+        for k, name in enumerate(steps):
+            t = rel[who, ATTN_SLOT + k] - qkv_end
+            lines.append(f"| {name} | {np.median(t):+.2f} | {t.max():+.2f} |")
     return lines + [""]
 
 

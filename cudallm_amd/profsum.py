@@ -1,13 +1,17 @@
 """Summaries of rocprofv3 output for this library's kernels (the tables under profiles/).
 
     python -m cudallm_amd.profsum trace DIR [--matvec-blocks WTYPE] [--decode [--skip N] [--take K]]
+    python -m cudallm_amd.profsum trace DIR --graph-runs LABEL,LABEL,... [--steps K] [--prompt P]
     python -m cudallm_amd.profsum counters FETCH_DIR WRITE_DIR [--calib-bytes N]
 
 ``trace``: reads DIR/*kernel_trace.csv (rocprofv3 --kernel-trace).  With --matvec-blocks the matvec dispatches are
 split into contiguous runs of one kernel name (cudallm_amd.kernelbench --op shapes launches qkv, wo, gate_up, down,
 lm_head in that order, and consecutive shapes use different kernel instances), and each run is matched to its shape
 by position; per run: calls, mean / median / min / max duration, and GB/s and the fraction of 8 TB/s from the shape's
-algorithmic bytes.  With --decode: the persistent decode kernels per weight type.
+algorithmic bytes.  With --decode: the persistent decode kernels per weight type.  With --graph-runs (the output of
+cudallm_amd.graphbench): per weight type, the decode dispatches split into runs of P prompt + K timed steps, one per
+label; per run the timed steps' mean duration and the gaps between consecutive dispatches (start minus the previous
+end).
 
 ``counters``: two rocprofv3 --pmc runs (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch); each counter is scaled by
 what it reads for the largest __amd_rocclr_copyBuffer dispatch of known size (--calib-bytes, the bench's
@@ -92,6 +96,31 @@ def decode_stats(rows, skip: int = 0, take: int = 0):
     return out
 
 
+def graph_runs(rows, labels: list[str], steps: int, prompt: int = 16):
+    per = {}
+    for r in sorted(rows, key=lambda r: int(r["Start_Timestamp"])):
+        if "decode_kernel" not in r["Kernel_Name"]:
+            continue
+        st, en = int(r["Start_Timestamp"]), int(r["End_Timestamp"])
+        if (en - st) / 1e3 < PROBE_US:
+            continue
+        per.setdefault(_dtype(r["Kernel_Name"]), []).append((st, en))
+    out = {}
+    for wd, d in per.items():
+        runs = {}
+        for i, label in enumerate(labels):
+            run = d[i * (prompt + steps) + prompt:(i + 1) * (prompt + steps)]
+            if len(run) < 2:
+                continue
+            gaps = [(run[k + 1][0] - run[k][1]) / 1e3 for k in range(len(run) - 1)]
+            durs = [(e - s) / 1e3 for s, e in run]
+            runs[label] = {"steps": len(run), "mean_us": statistics.fmean(durs), "gap_median_us": statistics.median(gaps),
+                           "gap_mean_us": statistics.fmean(gaps), "gap_max_us": max(gaps),
+                           "span_us_per_step": (run[-1][1] - run[0][0]) / 1e3 / len(run)}
+        out[wd] = runs
+    return out
+
+
 def counters(fetch_dir: Path, write_dir: Path, calib_bytes: int):
     def load(d, counter):
         rows = [r for r in _rows(d, "counter_collection.csv") if r["Counter_Name"] == counter]
@@ -129,6 +158,9 @@ def main(argv=None) -> int:
     t.add_argument("--decode", action="store_true")
     t.add_argument("--skip", type=int, default=0, help="decode: drop each weight type's first N steps")
     t.add_argument("--take", type=int, default=0, help="decode: then keep N steps (0 = all)")
+    t.add_argument("--graph-runs", help="comma-separated labels of cudallm_amd.graphbench's runs, in order")
+    t.add_argument("--steps", type=int, default=256, help="graph runs: timed steps per run")
+    t.add_argument("--prompt", type=int, default=16, help="graph runs: untimed prompt steps before each run")
     c = sub.add_parser("counters")
     c.add_argument("fetch_dir", type=Path)
     c.add_argument("write_dir", type=Path)
@@ -141,6 +173,8 @@ def main(argv=None) -> int:
             res["matvec"] = matvec_blocks(rows, args.matvec_blocks)
         if args.decode:
             res["decode"] = decode_stats(rows, args.skip, args.take)
+        if args.graph_runs:
+            res["graph_runs"] = graph_runs(rows, args.graph_runs.split(","), args.steps, args.prompt)
     else:
         res = counters(args.fetch_dir, args.write_dir, args.calib_bytes)
     print(json.dumps(res, indent=1))
