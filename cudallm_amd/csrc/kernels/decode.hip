@@ -52,6 +52,7 @@ constexpr unsigned kEpochStride = 256;   // tag slots per step
 constexpr unsigned kSpinCap = 1u << 20;     // bounded waits on other workgroups (~1 s of polling)
 constexpr unsigned kLdsSpinCap = 1u << 26;  // bounded waits inside the workgroup (a few seconds)
 constexpr int kPartStride = HD + 2;      // o[64], m, l
+constexpr int kMergeOneWave = 16;        // split merges up to this many splits take one wave per head
 constexpr int kPairs = QKV / 2;          // RoPE pairs (i, i+32) of every q/k/v head
 // Tuning knobs of the decode kernel, overridable at build time (cudallm_amd/sweep_decode.py sweeps them): lines in
 // flight per loader wave, ring slots per compute wave and lm_head rows per unit (each for bf16 / quantised).
@@ -1169,6 +1170,80 @@ __device__ __noinline__ void merge_long(const uint64_t* tpart, uint64_t* tatt, u
     }
 }
 
+    // 17 to 64 splits: one workgroup per head, its splits spread over the 4 waves.  Head h goes to the
+    // workgroup whose attention index (ab above) is G - 32 + h: tasks are dealt in ab order, so these 32 hold
+    // the fewest (none up to 28 splits) and start polling first.  Wave w takes splits w Q .. w Q + Q - 1
+    // (Q <= 16): every (m, l) and o value in flight at once, one round trip, where one wave per head needed
+    // up to four (at 8000 positions, bf16 1361 -> 1547 tok/s on MI355X).  Each wave merges its splits in order
+    // against its own maximum, then wave 0 adds the 4 partials in wave order, rescaled to the head's maximum:
+    // out = sum_w e^(M_w - M) acc_w / sum_w e^(M_w - M) L_w.  Up to 16 splits the one-wave merge above is
+    // faster (its single round has no barrier or LDS step: 7-12 us per step at 2-3 splits).
+// Inlined: out of line, its call made the whole step 26-52 us slower on MI355X (the call constrains the caller's
+// register allocation around it), where inlined it costs 1-6 us per step at short contexts, which never run it.
+template <WType WT>
+__device__ __forceinline__ void merge_par(Smem<WT>& sm, const uint64_t* tpart, uint64_t* tatt, unsigned tg, int nsplit, int NS,
+                                       unsigned& ep, unsigned ep_in, bool& lbad, unsigned* err, int wave, int lane) {
+    const int G = gridDim.x, h = (static_cast<int>(blockIdx.x) + G / 2) % G - (G - NH);
+    if (h >= 0) {
+        const int Q = (nsplit + kCW - 1) / kCW, s0 = wave * Q, cnt = max(0, min(Q, nsplit - s0));
+        const uint64_t* pp = tpart + (static_cast<size_t>(h) * NS + s0) * kPartStride;
+        const unsigned tag = tg + T_ATT_PART;
+        uint64_t vm = static_cast<uint64_t>(tag) << 32, vl = vm;
+        if (lane < cnt) {
+            vm = tload(pp + lane * kPartStride + HD);
+            vl = tload(pp + lane * kPartStride + HD + 1);
+        }
+        uint64_t v[16];
+#pragma unroll
+        for (int k = 0; k < 16; ++k)
+            v[k] = k < cnt ? tload(pp + k * kPartStride + lane) : static_cast<uint64_t>(tag) << 32;
+        unsigned spins = 0;
+        for (;;) {
+            bool ok = tagged(vm, tag) && tagged(vl, tag);
+#pragma unroll
+            for (int k = 0; k < 16; ++k) ok = ok && tagged(v[k], tag);
+            if (ok || give_up(spins, err)) break;
+            if (!tagged(vm, tag)) vm = tload(pp + lane * kPartStride + HD);
+            if (!tagged(vl, tag)) vl = tload(pp + lane * kPartStride + HD + 1);
+#pragma unroll
+            for (int k = 0; k < 16; ++k)
+                if (k < cnt && !tagged(v[k], tag)) v[k] = tload(pp + k * kPartStride + lane);
+        }
+        float* macc = sm.big + kAttnQ;          // [4][64] the waves' partial o sums
+        float* mml = sm.big + kAttnQ + 4 * HD;  // [4][2] their maxima and l sums
+        cwait(sm.bar, ep_in, lbad);  // every wave has read the qkv input (this region may hold it)
+        if (cnt > 0) {
+            const float ms = lane < cnt ? tvalue(vm) : -INFINITY, ls = lane < cnt ? tvalue(vl) : 0.f;
+            const float Mw = wave_max(ms);
+            const float e = lane < cnt ? expf(ms - Mw) : 0.f;
+            const float Lw = wave_sum(ls * e);
+            float acc = 0.f;
+#pragma unroll
+            for (int k = 0; k < 16; ++k)
+                if (k < cnt) acc = fmaf(tvalue(v[k]), __shfl(e, k), acc);
+            macc[wave * HD + lane] = acc;
+            if (lane == 0) {
+                mml[2 * wave] = Mw;
+                mml[2 * wave + 1] = Lw;
+            }
+        }
+        cbar(sm.bar, ep, wave, lane, lbad);
+        if (wave == 0) {
+            const int nw = (nsplit + Q - 1) / Q;  // waves that hold splits
+            float M = mml[0];
+            for (int w = 1; w < nw; ++w) M = fmaxf(M, mml[2 * w]);
+            float L = 0.f, acc = 0.f;
+            for (int w = 0; w < nw; ++w) {
+                const float f = expf(mml[2 * w] - M);
+                L = fmaf(f, mml[2 * w + 1], L);
+                acc = fmaf(f, macc[w * HD + lane], acc);
+            }
+            tstore(tatt + h * HD + lane, acc / L, tg + T_ATT);
+        }
+        cbar(sm.bar, ep, wave, lane, lbad);  // macc / mml are read before anything overwrites them
+    }
+}
+
 // ---- the kernel ------------------------------------------------------------------------------
 
 template <WType WT>
@@ -1516,11 +1591,11 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
         }
         stamp(p, 1 + 6 * l + 1);
 
-        // ---- LSE merge of the splits: one wave per head ----
+        // ---- LSE merge of the splits ----
         renew();
-        if (nsplit > 1 && nsplit <= kWave) {
-            // Lane s holds split s; one round trip for the first 16 splits: each lane's (m, l) and the o values
-            // all in flight at once.
+        if (nsplit > 1 && nsplit <= kMergeOneWave) {
+            // Up to 16 splits, one wave per head: lane s holds split s, and each lane's (m, l) and the o values of
+            // every split are in flight at once (one round trip).
 #pragma unroll 1
             for (int h = gw; h < NH; h += NW) {
                 const uint64_t* pp = tpart + static_cast<size_t>(h) * NS * kPartStride;
@@ -1532,7 +1607,7 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
                 }
                 float M = 0.f, e = 0.f, Lsum = 0.f, acc = 0.f;
 #pragma unroll 1
-                for (int sb = 0; sb < nsplit; sb += 16) {
+                for (int sb = 0; sb < nsplit; sb += kMergeOneWave) {
                     uint64_t v[16];
 #pragma unroll
                     for (int k = 0; k < 16; ++k)
@@ -1562,6 +1637,8 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
                 }
                 tstore(tatt + h * HD + lane, acc / Lsum, tg + T_ATT);
             }
+        } else if (nsplit > kMergeOneWave && nsplit <= kWave) {
+            merge_par(sm, tpart, tatt, tg, nsplit, NS, ep, ep_in, lbad, err, wave, lane);
         } else if (nsplit > kWave) {
             merge_long(tpart, tatt, tg, nsplit, NS, gw, NW, lane, err);
         }

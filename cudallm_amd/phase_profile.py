@@ -20,9 +20,14 @@ import numpy as np
 PHASES = ["qkv", "attention", "merge", "wo", "gate_up", "down"]
 
 
+def max_seq_for(ctx: int) -> int:
+    """The engine's context: 4096, or the next multiple of 4096 that holds ctx."""
+    return max(4096, -(-(ctx + 1) // 4096) * 4096)
+
+
 def profile(path, ctx: int, reps: int):
     from . import engine as E
-    with E.Engine(path, max_seq_len=4096) as eng:
+    with E.Engine(path, max_seq_len=max_seq_for(ctx)) as eng:
         eng.step_async(128000)
         for _ in range(ctx - 2):
             eng.step_async(None)
@@ -108,7 +113,7 @@ def main(argv=None) -> int:
     with tempfile.TemporaryDirectory(dir="/dev/shm" if Path("/dev/shm").is_dir() else None) as d:
         for wd in args.dtypes.split(","):
             path = Path(d) / f"profile_{wd}.cudallm"
-            synth.write_model(path, wd, seed=1234)
+            synth.write_model(path, wd, seed=1234, max_seq_len=max_seq_for(args.ctx))
             S = profile(path, args.ctx, args.reps)
             if args.raw:
                 args.raw.mkdir(parents=True, exist_ok=True)
