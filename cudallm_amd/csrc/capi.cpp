@@ -135,8 +135,8 @@ void enqueue_matvec(int weight_dtype, int epilogue, int rpb, const void* w, cons
     need(rpb == 0 || rpb == 1 || rpb == 2 || rpb == 4 || rpb == 8, "rpb must be 0, 1, 2, 4 or 8");
     need(wt != cllm::WType::INT4 || cols % 128 == 0, "int4 weights need cols to be a multiple of 128");
     const cllm::MatvecArgs a{w, scales, x, norm_w, eps, y, rows, cols};
-    cllm::launch_matvec(wt, static_cast<cllm::Epilogue>(epilogue), a, rpb ? rpb : cllm::default_rpb(wt),
-                        static_cast<hipStream_t>(stream));
+    const auto ep = static_cast<cllm::Epilogue>(epilogue);
+    cllm::launch_matvec(wt, ep, a, rpb ? rpb : cllm::default_rpb(wt, ep, rows, cols), static_cast<hipStream_t>(stream));
 }
 
 }  // namespace
@@ -288,7 +288,7 @@ int cudallm_kernel_matvec(int impl, int weight_dtype, int epilogue, int fuse_nor
         if (impl == 0)
             cllm::launch_matvec_naive(a, nullptr);
         else
-            cllm::launch_matvec(wt, ep, a, rpb ? rpb : cllm::default_rpb(wt), nullptr);
+            cllm::launch_matvec(wt, ep, a, rpb ? rpb : cllm::default_rpb(wt, ep, rows, cols), nullptr);
         st.finish();
     });
 }
@@ -406,6 +406,21 @@ int cudallm_launch_matvec_timed(int weight_dtype, int epilogue, int rpb, const v
         } disarm;
         cllm::arm_kernel_events(static_cast<hipEvent_t>(start_event), static_cast<hipEvent_t>(stop_event));
         enqueue_matvec(weight_dtype, epilogue, rpb, w, scales, x, norm_w, eps, y, rows, cols, stream);
+    });
+}
+
+int cudallm_launch_stream_read_timed(const void* src, unsigned long long bytes, int blocks_per_cu, unsigned* sink,
+                                     unsigned long long sink_words, void* stream, void* start_event, void* stop_event) {
+    return abi_entry("cudallm_launch_stream_read_timed", [&] {
+        need(src && sink, "src and sink are required");
+        need(start_event && stop_event, "start_event and stop_event are required");
+        need(bytes >= (1ull << 20) && bytes % 16 == 0, "bytes must be >= 1 MiB and a multiple of 16");
+        need(blocks_per_cu == 4 || blocks_per_cu == 8 || blocks_per_cu == 16, "blocks_per_cu must be 4, 8 or 16");
+        struct Disarm {
+            ~Disarm() { cllm::take_kernel_events(); }
+        } disarm;
+        cllm::arm_kernel_events(static_cast<hipEvent_t>(start_event), static_cast<hipEvent_t>(stop_event));
+        cllm::launch_stream_read(src, bytes, blocks_per_cu, sink, sink_words, static_cast<hipStream_t>(stream));
     });
 }
 

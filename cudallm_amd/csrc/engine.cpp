@@ -110,7 +110,7 @@ Engine::Engine(const std::string& path, const EngineOptions& opts) : opts_(opts)
     weights_ = std::make_unique<Weights>(path);
     const ModelConfig& c = weights_->config();
     max_seq_ = opts_.max_seq_len ? opts_.max_seq_len : c.max_seq_len;
-    rpb_ = opts_.matvec_rpb ? opts_.matvec_rpb : default_rpb(c.wt);
+    rpb_ = opts_.matvec_rpb;  // 0: the library's per-shape choice (default_rpb)
     step_limit_ = env_step_limit();
     try {
         CLLM_HIP(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
@@ -276,7 +276,8 @@ void Engine::build_program() {
             CLLM_INTERNAL(ep == Epilogue::STORE && !norm_w, "naive matvec: STORE without a fused norm only");
             emit([a](hipStream_t s) { launch_matvec_naive(a, s); });
         } else {
-            emit([a, wt, ep, rpb](hipStream_t s) { launch_matvec(wt, ep, a, rpb, s); });
+            const int r = rpb ? rpb : default_rpb(wt, ep, a.rows, a.cols);
+            emit([a, wt, ep, r](hipStream_t s) { launch_matvec(wt, ep, a, r, s); });
         }
     };
     float *x = x_, *xb = xb_, *qkv = qkv_, *att = att_, *tmp = tmp_, *gu = gu_, *act = act_;

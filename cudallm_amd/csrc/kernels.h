@@ -23,7 +23,8 @@ struct MatvecArgs {
     int rows, cols;
 };
 
-int default_rpb(WType wt);
+// rpb of the fast matvec when the caller passes 0 (per weight type and shape).
+int default_rpb(WType wt, Epilogue ep, int rows, int cols);
 // Events the next matvec launch on this thread records at its kernel's start and end (benchmarks: the interval
 // excludes the launch gap).  take_kernel_events() returns and clears them.
 struct KernelEvents {
@@ -81,5 +82,10 @@ struct ReadBandwidth {
     int blocks_per_cu = 0, loads_in_flight = 0;
 };
 ReadBandwidth measure_read_bandwidth(size_t bytes, int reps);
+// One stream read of `bytes` at `src` (the bandwidth kernel: blocks_per_cu x CUs workgroups, 8 loads in flight per
+// thread; sink: blocks_per_cu x CUs words, written only for a value the data never holds in practice).  Records the
+// armed kernel events, like launch_matvec.
+void launch_stream_read(const void* src, size_t bytes, int blocks_per_cu, unsigned* sink, size_t sink_words,
+                        hipStream_t s);
 
 }  // namespace cllm

@@ -9,6 +9,8 @@
 #include <algorithm>
 #include <vector>
 
+#include <hip/hip_ext.h>
+
 #include "../kernels.h"
 #include "device.h"
 
@@ -37,6 +39,24 @@ __global__ void __launch_bounds__(kBwThreads) stream_read_kernel(const u32x4* sr
 }
 
 }  // namespace
+
+void launch_stream_read(const void* src, size_t bytes, int blocks_per_cu, unsigned* sink, size_t sink_words,
+                        hipStream_t s) {
+    CLLM_REQUIRE(src && sink, "stream read: src and sink are required");
+    CLLM_REQUIRE(bytes >= (1u << 20) && bytes % 16 == 0, "stream read: bytes must be >= 1 MiB and a multiple of 16");
+    CLLM_REQUIRE(blocks_per_cu == 4 || blocks_per_cu == 8 || blocks_per_cu == 16, "stream read: blocks_per_cu is 4, 8 or 16");
+    const int grid = blocks_per_cu * device_cu_count();
+    CLLM_REQUIRE(sink_words >= static_cast<size_t>(grid), "stream read: sink needs blocks_per_cu x CUs words");
+    const size_t n16 = bytes / 16, per_block = (n16 + grid - 1) / grid;
+    const u32x4* p = static_cast<const u32x4*>(src);
+    const KernelEvents ev = take_kernel_events();
+    if (ev.start)
+        hipExtLaunchKernelGGL(stream_read_kernel<8>, dim3(grid), dim3(kBwThreads), 0, s, ev.start, ev.stop, 0u, p, n16,
+                              per_block, sink);
+    else
+        hipLaunchKernelGGL(stream_read_kernel<8>, dim3(grid), dim3(kBwThreads), 0, s, p, n16, per_block, sink);
+    CLLM_HIP(hipGetLastError());
+}
 
 ReadBandwidth measure_read_bandwidth(size_t bytes, int reps) {
     CLLM_REQUIRE(bytes >= (64u << 20) && bytes % 16 == 0, "read bandwidth: bytes must be >= 64 MiB and a multiple of 16");

@@ -73,6 +73,8 @@ SIGNATURES = {
     "cudallm_kernel_argmax": ([_F32P, c_int, _I32P], c_int),
     "cudallm_launch_matvec": ([c_int, c_int, c_int] + [c_void_p] * 4 + [c_float, c_void_p, c_int, c_int, c_void_p],
                               c_int),
+    "cudallm_launch_stream_read_timed": ([c_void_p, c_ulonglong, c_int, c_void_p, c_ulonglong, c_void_p, c_void_p,
+                                          c_void_p], c_int),
     "cudallm_launch_matvec_timed": ([c_int, c_int, c_int] + [c_void_p] * 4 + [c_float, c_void_p, c_int, c_int] +
                                     [c_void_p] * 3, c_int),
     "cudallm_launch_attention": ([c_void_p] * 7 + [c_int] * 4 + [c_void_p], c_int),
@@ -330,6 +332,13 @@ def launch_matvec_timed(wtype, epilogue, rpb: int, w_ptr: int, scales_ptr: int |
     """launch_matvec whose kernel records the two hipEvent_t handles at its own start and end."""
     call("cudallm_launch_matvec_timed", _code(WEIGHT_CODES, wtype), _code(EPILOGUE_CODES, epilogue), int(rpb), w_ptr,
          scales_ptr, x_ptr, norm_ptr, float(eps), y_ptr, int(rows), int(cols), stream, start_event, stop_event)
+
+
+def launch_stream_read_timed(src_ptr: int, nbytes: int, blocks_per_cu: int, sink_ptr: int, sink_words: int,
+                             stream: int | None, start_event: int, stop_event: int) -> None:
+    """One stream read of nbytes at src_ptr whose kernel records the two hipEvent_t handles at its start and end."""
+    call("cudallm_launch_stream_read_timed", src_ptr, int(nbytes), int(blocks_per_cu), sink_ptr, int(sink_words), stream,
+         start_event, stop_event)
 
 
 def launch_attention(q_ptr: int, k_ptr: int, v_ptr: int, pos_ptr: int, part_o_ptr: int, part_ml_ptr: int, out_ptr: int,

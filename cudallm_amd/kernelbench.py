@@ -2,14 +2,16 @@
 --op matvec|shapes, src/tools/cudallm_kernelbench.cpp:115-180,253-298).
 
     python -m cudallm_amd.kernelbench --op shapes --wtype {bf16,int8,int4} [--rpb 1|2|4|8] [--iters 200] [--json PATH]
+                                      [--stream]
     python -m cudallm_amd.kernelbench --op matvec --wtype W --rows R --cols C [--epilogue store|add|swiglu]
-                                      [--fuse-norm] [--rpb N] [--iters 200] [--json PATH]
+                                      [--fuse-norm] [--rpb N] [--iters 200] [--json PATH] [--stream]
 
 Same operands as the reference (weights N(0, 0.02) as bf16, random int8 / packed int4 with scales, x N(0, 1),
 norm weights U(0.5, 1.5)), same five model shapes and epilogues, same JSON fields (median_us per launch, GB/s,
 weighted_us = 16 (qkv + wo + gate_up + down) + lm_head).  One difference, for MI355X: each launch reads a different
 copy of the weights, rotating over more than 1.5 GiB, so that the 256 MB Infinity Cache cannot serve a shape
-that the reference's single copy would leave cache-resident.
+that the reference's single copy would leave cache-resident.  With --stream, each shape's weight bytes are also read
+by the bandwidth kernel over the same copies (stream_us): the time a plain read of those bytes takes at that size.
 """
 import argparse
 import json
@@ -22,8 +24,14 @@ SHAPES = [("qkv", 3072, 2048, "store", True), ("wo", 2048, 2048, "add", False),
           ("gate_up", 16384, 2048, "swiglu", True), ("down", 2048, 8192, "add", False),
           ("lm_head", 128256, 2048, "store", True)]
 RPBS = (1, 2, 4, 8)
-# The library's choice when rpb = 0 (default_rpb in csrc/kernels/small.hip).
-DEFAULT_RPB = {"bf16": 2, "int8": 4, "int4": 4}
+# The library's choice when rpb = 0 (kDefaultRpb / default_rpb in csrc/kernels/small.hip), per weight type and shape
+# class: other, SwiGLU, 8192 columns, >= 65536 rows.
+DEFAULT_RPB = {"bf16": (2, 1, 8, 2), "int8": (4, 4, 4, 4), "int4": (4, 8, 4, 8)}
+
+
+def default_rpb(wd: str, ep: str, rows: int, cols: int) -> int:
+    cls = 1 if ep == "swiglu" else 2 if cols >= 8192 else 3 if rows >= 65536 else 0
+    return DEFAULT_RPB[wd][cls]
 PEAK_GBPS = 8000.0
 
 
@@ -38,9 +46,10 @@ def matvec_bytes(wd: str, rows: int, cols: int) -> int:
 
 
 def bench_matvec(wd: str, name: str, rows: int, cols: int, ep: str, norm: bool, iters: int, rpb: int = 0,
-                 rotate_bytes: float = 1.5 * (1 << 30)) -> dict:
+                 rotate_bytes: float = 1.5 * (1 << 30), stream: bool = False) -> dict:
     """Time `iters` launches on torch's current stream, rotating over weight copies totalling at least `rotate_bytes`.
-    Each kernel's duration comes from events its own dispatch records at the kernel's start and end.  Returns the
+    Each kernel's duration comes from events its own dispatch records at the kernel's start and end.  With `stream`,
+    the same copies' weight bytes are also read by the bandwidth kernel (stream_read).  Returns the
     reference's fields (median_us, gbps) plus the mean kernel time (avg_us), the wall time per launch including the
     launch gap, and the copy count."""
     import torch
@@ -95,12 +104,45 @@ def bench_matvec(wd: str, name: str, rows: int, cols: int, ep: str, norm: bool, 
     per = [a.elapsed_time(b) * 1e3 for a, b in kev]
     med, avg = statistics.median(per), statistics.fmean(per)
     wall = w0.elapsed_time(w1) * 1e3 / iters
+    rec = {"name": name, "rows": rows, "cols": cols, "impl": "opt", "wtype": wd, "epilogue": ep, "fuse_norm": norm,
+           "rpb": rpb or default_rpb(wd, ep, rows, cols), "bytes": nbytes, "median_us": med, "gbps": nbytes / med / 1e3,
+           "avg_us": avg, "gbps_avg": nbytes / avg / 1e3, "frac_of_8tbs": nbytes / avg / 1e3 / PEAK_GBPS,
+           "wall_us_per_launch": wall,
+           "copies": copies, "timing": "kernel start/end events recorded by the dispatch (hipExtLaunchKernel)"}
+    if stream:
+        rec.update(stream_read(ws, iters, sp))
+        rec["frac_of_stream"] = rec["gbps_avg"] / rec["stream_gbps"]
     del ws, ss
     torch.cuda.empty_cache()
-    return {"name": name, "rows": rows, "cols": cols, "impl": "opt", "wtype": wd, "epilogue": ep, "fuse_norm": norm,
-            "rpb": rpb or DEFAULT_RPB[wd], "bytes": nbytes, "median_us": med, "gbps": nbytes / med / 1e3,
-            "avg_us": avg, "frac_of_8tbs": nbytes / avg / 1e3 / PEAK_GBPS, "wall_us_per_launch": wall,
-            "copies": copies, "timing": "kernel start/end events recorded by the dispatch (hipExtLaunchKernel)"}
+    return rec
+
+
+STREAM_BLOCKS = (4, 8, 16)  # the bandwidth kernel's launch shapes (workgroups per CU)
+
+
+def stream_read(tensors, iters: int, sp: int) -> dict:
+    """The bandwidth kernel reading each launch's weight tensor (its bytes rounded down to 16), over the same rotation
+    of copies, timed by the dispatch like the matvec; the fastest of its launch shapes (mean kernel time).  What a
+    plain read of the same bytes takes bounds what the matvec can reach."""
+    import torch
+    from . import engine as E
+    sink = torch.zeros(16 * 1024, dtype=torch.int32, device="cuda")
+    stream = torch.cuda.current_stream()
+    nb = (tensors[0].numel() * tensors[0].element_size()) // 16 * 16
+    best = None
+    for bpc in STREAM_BLOCKS:
+        kev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(iters + 5)]
+        for a, b in kev:
+            a.record(stream)
+            b.record(stream)
+        for i, (a, b) in enumerate(kev):  # the first 5 are warm-up
+            E.launch_stream_read_timed(tensors[i % len(tensors)].data_ptr(), nb, bpc, sink.data_ptr(), sink.numel(), sp,
+                                       a.cuda_event, b.cuda_event)
+        kev[-1][1].synchronize()
+        avg = statistics.fmean(a.elapsed_time(b) * 1e3 for a, b in kev[5:])
+        if best is None or avg < best[1]:
+            best = (bpc, avg)
+    return {"stream_bytes": nb, "stream_us": best[1], "stream_blocks_per_cu": best[0], "stream_gbps": nb / best[1] / 1e3}
 
 
 def weighted_us(per_shape_us: dict) -> float:
@@ -109,13 +151,14 @@ def weighted_us(per_shape_us: dict) -> float:
         per_shape_us["lm_head"]
 
 
-def bench_shapes(wd: str, rpb: int = 0, iters: int = 200) -> dict:
+def bench_shapes(wd: str, rpb: int = 0, iters: int = 200, stream: bool = False) -> dict:
     """--op shapes: the five model shapes with the fused engine's epilogues."""
     import torch
-    results = [bench_matvec(wd, name, rows, cols, ep, norm, iters if name != "lm_head" else max(10, iters // 4), rpb)
+    results = [bench_matvec(wd, name, rows, cols, ep, norm, iters if name != "lm_head" else max(10, iters // 4), rpb,
+                            stream=stream)
                for name, rows, cols, ep, norm in SHAPES]
     return {"tool": "cudallm_kernelbench", "op": "shapes", "gpu_name": torch.cuda.get_device_name(0), "iters": iters,
-            "impl": "opt", "wtype": wd, "rpb": rpb or DEFAULT_RPB[wd], "results": results,
+            "impl": "opt", "wtype": wd, "rpb": rpb or "per shape", "results": results,
             "weighted_us": weighted_us({r["name"]: r["median_us"] for r in results})}
 
 
@@ -130,6 +173,8 @@ def main(argv=None) -> int:
     ap.add_argument("--fuse-norm", action="store_true")
     ap.add_argument("--iters", type=int, default=200)
     ap.add_argument("--json", type=Path)
+    ap.add_argument("--stream", action="store_true",
+                    help="also time the bandwidth kernel reading the same weight bytes (stream_us, frac_of_stream)")
     args = ap.parse_args(argv)
     if args.iters < 1:
         ap.error("--iters must be >= 1")
@@ -138,14 +183,16 @@ def main(argv=None) -> int:
             ap.error("--rows and --cols are required for --op matvec")
         import torch
         r = bench_matvec(args.wtype, "matvec", args.rows, args.cols, args.epilogue, args.fuse_norm, args.iters,
-                         args.rpb)
+                         args.rpb, stream=args.stream)
         rec = {"tool": "cudallm_kernelbench", "op": "matvec", "gpu_name": torch.cuda.get_device_name(0),
                "iters": args.iters, "impl": "opt", "wtype": args.wtype, "rpb": r["rpb"], "results": [r]}
     else:
-        rec = bench_shapes(args.wtype, args.rpb, args.iters)
+        rec = bench_shapes(args.wtype, args.rpb, args.iters, stream=args.stream)
     for r in rec["results"]:
         print(f"{r['name']:8s} {r['rows']:6d}x{r['cols']:<5d} {r['wtype']:4s} {r['epilogue']:6s} norm={int(r['fuse_norm'])} "
-              f"rpb={r['rpb']}: {r['median_us']:8.2f} us  {r['gbps']:7.1f} GB/s", flush=True)
+              f"rpb={r['rpb']}: {r['median_us']:8.2f} us  {r['gbps']:7.1f} GB/s"
+              + (f"  (stream read of the weights: {r['stream_us']:.2f} us, {r['stream_gbps']:.0f} GB/s)" if "stream_us" in r
+                 else ""), flush=True)
     if "weighted_us" in rec:
         print(f"weighted_us = 16*(qkv+wo+gate_up+down) + lm_head = {rec['weighted_us']:.2f}", flush=True)
     if args.json:

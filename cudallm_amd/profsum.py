@@ -1,6 +1,7 @@
 """Summaries of rocprofv3 output for this library's kernels (the tables under profiles/).
 
     python -m cudallm_amd.profsum trace DIR [--matvec-blocks WTYPE] [--decode [--skip N] [--take K]]
+                                            [--bench-legs STEPS,WARMUP]
     python -m cudallm_amd.profsum trace DIR --graph-runs LABEL,LABEL,... [--steps K] [--prompt P]
     python -m cudallm_amd.profsum counters FETCH_DIR WRITE_DIR [--calib-bytes N]
 
@@ -55,22 +56,34 @@ def _stats(us):
             "max_us": max(us)}
 
 
+STREAM_WARMUP = 5  # kernelbench's stream_read launches this many untimed reads per launch shape
+
+
 def matvec_blocks(rows, wtype: str):
-    disp = [r for r in rows if "matvec" in r["Kernel_Name"]]
+    """Matvec dispatches in contiguous runs of one kernel name, matched to SHAPES by position; the bandwidth kernel's
+    dispatches after a shape's run (kernelbench --stream) are that shape's stream reads, per launch shape (grid size),
+    of which the fastest shape's mean (warm-up dropped) is reported."""
     blocks = []
-    for r in disp:
+    for r in sorted(rows, key=lambda r: int(r["Start_Timestamp"])):
+        name = r["Kernel_Name"]
         us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
-        if blocks and blocks[-1][0] == r["Kernel_Name"]:
-            blocks[-1][1].append(us)
-        else:
-            blocks.append((r["Kernel_Name"], [us]))
+        if "matvec" in name:
+            if blocks and blocks[-1][0] == name and not blocks[-1][2]:
+                blocks[-1][1].append(us)
+            else:
+                blocks.append((name, [us], {}))
+        elif "stream_read_kernel" in name and blocks:
+            blocks[-1][2].setdefault(r.get("Grid_Size_X", "?"), []).append(us)
     out = []
-    for (name, us), shape in zip(blocks, SHAPES):
+    for (name, us, streams), shape in zip(blocks, SHAPES):
         sname, rws, cols, ep, norm = shape
         st = _stats(us)
         b = matvec_bytes(wtype, rws, cols)
         st.update(shape=sname, rows=rws, cols=cols, kernel=name.split("(")[0], bytes=b,
                   gbps=b / st["mean_us"] / 1e3, frac_of_8tbs=b / st["mean_us"] / 1e3 / (PEAK / 1e9))
+        means = [statistics.fmean(v[STREAM_WARMUP:]) for v in streams.values() if len(v) > STREAM_WARMUP]
+        if means:
+            st["stream_mean_us"] = min(means)
         out.append(st)
     return out
 
@@ -78,10 +91,8 @@ def matvec_blocks(rows, wtype: str):
 PROBE_US = 50.0  # the engine's co-residency probe launch of the decode kernel takes a few microseconds
 
 
-def decode_stats(rows, skip: int = 0, take: int = 0):
-    """Decode steps per weight type, in dispatch order; the co-residency probe launches (same kernel, under PROBE_US)
-    are counted apart.  `skip` drops each weight type's first steps and `take` (when > 0) keeps the next `take`:
-    bench.py's timed region is steps PROMPT + warmup + 1 .. + steps (skip = 16 + warmup, take = steps)."""
+def _decode_launches(rows):
+    """Durations (us) of the decode kernel's launches per weight type in dispatch order, and its probe launches."""
     per, probes = {}, {}
     for r in sorted(rows, key=lambda r: int(r["Start_Timestamp"])):
         if "decode_kernel" not in r["Kernel_Name"]:
@@ -89,6 +100,37 @@ def decode_stats(rows, skip: int = 0, take: int = 0):
         wd = _dtype(r["Kernel_Name"])
         us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
         (probes if us < PROBE_US else per).setdefault(wd, []).append(us)
+    return per, probes
+
+
+def bench_legs(rows, steps: int, warmup: int, prompt: int = 16, c5_reps: int = 5, c5_warmup: int = 1, c5_gen: int = 256):
+    """bench.py's decode launches per weight type, split into its legs.  The decode leg launches a warm-up sequence
+    (prompt + warmup steps), the timed sequence's prompt, `steps` timed steps and one more step that returns the
+    last token; the config-5 leg then runs c5_warmup + c5_reps sequences of prompt + c5_gen steps, of which the
+    last c5_gen of each timed rep are timed."""
+    per, _ = _decode_launches(rows)
+    out = {}
+    for wd, us in per.items():
+        t0 = prompt + warmup + prompt
+        leg = {"decode_timed": _stats(us[t0:t0 + steps])}
+        c0 = t0 + steps + 1
+        c5 = []
+        for r in range(c5_warmup, c5_warmup + c5_reps):
+            s0 = c0 + r * (prompt + c5_gen) + prompt
+            c5 += us[s0:s0 + c5_gen]
+        if c5:
+            leg["config5_timed"] = _stats(c5)
+        leg["launches"] = len(us)
+        leg["expected_launches"] = c0 + (c5_warmup + c5_reps) * (prompt + c5_gen) if c5 else c0
+        out[wd] = leg
+    return out
+
+
+def decode_stats(rows, skip: int = 0, take: int = 0):
+    """Decode steps per weight type, in dispatch order; the co-residency probe launches (same kernel, under PROBE_US)
+    are counted apart.  `skip` drops each weight type's first steps and `take` (when > 0) keeps the next `take`.
+    bench_legs() gives the skip and take of bench.py's timed launches."""
+    per, probes = _decode_launches(rows)
     per = {wd: us[skip:skip + take] if take > 0 else us[skip:] for wd, us in per.items()}
     out = {wd: _stats(us) for wd, us in per.items() if us}
     for wd, us in probes.items():
@@ -158,6 +200,8 @@ def main(argv=None) -> int:
     t.add_argument("--decode", action="store_true")
     t.add_argument("--skip", type=int, default=0, help="decode: drop each weight type's first N steps")
     t.add_argument("--take", type=int, default=0, help="decode: then keep N steps (0 = all)")
+    t.add_argument("--bench-legs", metavar="STEPS,WARMUP",
+                   help="split bench.py's decode launches (run with --steps STEPS --warmup WARMUP) into its legs")
     t.add_argument("--graph-runs", help="comma-separated labels of cudallm_amd.graphbench's runs, in order")
     t.add_argument("--steps", type=int, default=256, help="graph runs: timed steps per run")
     t.add_argument("--prompt", type=int, default=16, help="graph runs: untimed prompt steps before each run")
@@ -173,6 +217,9 @@ def main(argv=None) -> int:
             res["matvec"] = matvec_blocks(rows, args.matvec_blocks)
         if args.decode:
             res["decode"] = decode_stats(rows, args.skip, args.take)
+        if args.bench_legs:
+            k, w = (int(v) for v in args.bench_legs.split(","))
+            res["bench_legs"] = bench_legs(rows, k, w)
         if args.graph_runs:
             res["graph_runs"] = graph_runs(rows, args.graph_runs.split(","), args.steps, args.prompt)
     else:

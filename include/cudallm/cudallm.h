@@ -163,6 +163,13 @@ int cudallm_launch_attention(const float* q, const unsigned short* k_cache, cons
  * and the median of the best shape.  No reference counterpart in C: the reference measures the same quantity with
  * its tool src/tools/cudallm_bandwidth.cpp:19-68 ("read_gbps_best", the peak its roofline fractions use). */
 int cudallm_measure_read_bandwidth(unsigned long long bytes, int reps, double* best_gbps, double* median_gbps);
+/* One read of `bytes` (>= 1 MiB, a multiple of 16) at device pointer `src` by the kernel above, with
+ * blocks_per_cu (4, 8 or 16) x CUs workgroups; its dispatch records start_event / stop_event at the kernel's start
+ * and end, as cudallm_launch_matvec_timed does.  `sink` is device memory of sink_words >= blocks_per_cu x CUs words
+ * that the kernel writes only if the data XOR-folds to one fixed word.  For kernel benchmarks: the read time of a
+ * matvec's own bytes, on the same copies, bounds what the matvec can reach.  No reference counterpart. */
+int cudallm_launch_stream_read_timed(const void* src, unsigned long long bytes, int blocks_per_cu, unsigned* sink,
+                                     unsigned long long sink_words, void* stream, void* start_event, void* stop_event);
 
 /* ---- weight quantisers on the GPU (no reference counterpart in C) ----
  * They replace the reference's offline numpy quantisers, python/cudallm/quantize.py:5-38, with

@@ -16,6 +16,7 @@ import pytest
 from cudallm_amd import eval_ppl as P
 from cudallm_amd import generate as G
 from cudallm_amd import kernelbench as K
+from cudallm_amd import profsum as PS
 from cudallm_amd import sweep_matvec as S
 
 VOCAB = 128256
@@ -150,9 +151,19 @@ def test_weighted_us_and_winner_rule():
 
 def test_default_rpb_matches_the_library():
     src = (Path(__file__).resolve().parents[1] / "cudallm_amd/csrc/kernels/small.hip").read_text()
-    body = src[src.index("int default_rpb(WType wt)"):]
-    got = {m.group(1).lower(): int(m.group(2)) for m in re.finditer(r"case WType::(\w+): return (\d+);", body[:400])}
+    body = src[src.index("constexpr int kDefaultRpb[3][4]"):]
+    got = {m.group(5): tuple(int(m.group(i)) for i in range(1, 5))
+           for m in re.finditer(r"\{(\d+), (\d+), (\d+), (\d+)\},\s*// (\w+)", body[:300])}
     assert got == K.DEFAULT_RPB
+    assert "ep == Epilogue::SWIGLU ? 1 : cols >= 8192 ? 2 : rows >= 65536 ? 3 : 0" in body
+    assert [K.default_rpb("bf16", ep, r, c) for _, r, c, ep, _ in K.SHAPES] == [2, 2, 1, 8, 2]
+    assert [K.default_rpb("int4", ep, r, c) for _, r, c, ep, _ in K.SHAPES] == [4, 4, 8, 4, 8]
+
+
+def test_shape_winners():
+    rec = lambda ts: {"results": [{"name": n, "avg_us": t} for n, t in zip(("qkv", "lm_head"), ts)]}
+    data = {"bf16": {"1": rec((5.0, 90.0)), "2": rec((5.0, 80.0)), "4": rec((4.0, 85.0))}}
+    assert S.shape_winners(data) == {"bf16": {"qkv": 4, "lm_head": 2}}
 
 
 def test_clis_parse():
@@ -227,3 +238,40 @@ def test_kernelbench_shapes_record(gpu):
         assert r["rpb"] == 2 and r["bytes"] == K.matvec_bytes("int4", rows, cols)
         assert 0 < r["median_us"] < 1e4 and r["gbps"] == pytest.approx(r["bytes"] / r["median_us"] / 1e3)
     torch.cuda.synchronize()
+
+
+def _row(name, start_us, dur_us, grid=65536):
+    return {"Kernel_Name": name, "Start_Timestamp": str(int(start_us * 1000)),
+            "End_Timestamp": str(int((start_us + dur_us) * 1000)), "Grid_Size_X": str(grid)}
+
+
+def test_profsum_matvec_blocks_with_stream_reads():
+    """Runs of one matvec kernel per shape, each followed by stream reads at two grid sizes (5 warm-up each)."""
+    rows, t = [], 0.0
+    for k, (name, r, c, ep, norm) in enumerate(K.SHAPES):
+        for _ in range(3):
+            rows.append(_row(f"void cllm::mv::matvec_fast<k{k}>(cllm::MatvecArgs)", t, 10.0 + k))
+            t += 20
+        for grid, dur in ((1024, 9.0), (2048, 8.0)):
+            for i in range(7):
+                rows.append(_row("stream_read_kernel<8>", t, 100.0 if i < 5 else dur, grid))
+                t += 200
+    out = PS.matvec_blocks(rows, "bf16")
+    assert [o["shape"] for o in out] == [s[0] for s in K.SHAPES]
+    assert [o["calls"] for o in out] == [3] * 5 and out[2]["mean_us"] == pytest.approx(12.0)
+    assert all(o["stream_mean_us"] == pytest.approx(8.0) for o in out)
+    assert out[0]["bytes"] == K.matvec_bytes("bf16", 3072, 2048)
+
+
+def test_profsum_bench_legs():
+    """bench.py's launch sequence: warm-up sequence, prompt, K timed, one more, then 6 config-5 sequences."""
+    K_, W = 3, 2
+    durs = [1.0] * (16 + W + 16) + [5.0] * K_ + [1.0]
+    for rep in range(6):
+        durs += [1.0] * 16 + [7.0 if rep else 3.0] * 256
+    rows = [_row("decode_kernel<(cllm::WType)4>", 1000.0 * i, 60.0 + d) for i, d in enumerate(durs)]
+    rows.append(_row("decode_kernel<(cllm::WType)4>", -100.0, 5.0))  # a co-residency probe
+    leg = PS.bench_legs(rows, K_, W)["int4"]
+    assert leg["decode_timed"]["calls"] == K_ and leg["decode_timed"]["mean_us"] == pytest.approx(65.0)
+    assert leg["config5_timed"]["calls"] == 1280 and leg["config5_timed"]["mean_us"] == pytest.approx(67.0)
+    assert leg["launches"] == leg["expected_launches"] == len(durs)

@@ -256,6 +256,19 @@ def test_matvec_hook_argument_errors(lib):
     assert ei.value.code == INVALID_ARG and "norm_w" in str(ei.value)
 
 
+def test_stream_read_hook_argument_errors(lib):
+    ev = ctypes.c_void_p(1)
+    assert lib.cudallm_launch_stream_read_timed(None, 1 << 20, 8, ctypes.c_void_p(1), 4096, None, ev, ev) == INVALID_ARG
+    assert lib.cudallm_launch_stream_read_timed(ctypes.c_void_p(1), 1000, 8, ctypes.c_void_p(1), 4096, None, ev,
+                                                ev) == INVALID_ARG
+    assert lib.cudallm_launch_stream_read_timed(ctypes.c_void_p(1), 1 << 20, 3, ctypes.c_void_p(1), 4096, None, ev,
+                                                ev) == INVALID_ARG
+    assert "blocks_per_cu" in lib.cudallm_last_error().decode()
+    assert lib.cudallm_launch_stream_read_timed(ctypes.c_void_p(1), 1 << 20, 8, ctypes.c_void_p(1), 4096, None, None,
+                                                ev) == INVALID_ARG
+    assert "start_event" in lib.cudallm_last_error().decode()
+
+
 def test_other_hook_argument_errors(lib):
     q = np.zeros(32 * 64, np.float32)
     kc = np.zeros((8, 128, 64), np.float16)

@@ -90,13 +90,32 @@ def test_matvec_model_shapes(wtype, name, rows, cols, epilogue, norm):
 
 
 @pytest.mark.parametrize("wtype", ["bf16", "int8", "int4"])
-@pytest.mark.parametrize("rows,cols", [(1000, 1024), (37, 3072), (130, 12288), (6, 2048), (10, 8192)])
+@pytest.mark.parametrize("rows,cols", [(1000, 1024), (37, 3072), (130, 12288), (6, 2048), (10, 8192), (20483, 2048)])
 @pytest.mark.parametrize("epilogue", ["store", "add", "swiglu"])
 def test_matvec_generic_and_ragged(wtype, rows, cols, epilogue):
-    """Widths other than 2048/8192 (LDS-staged path) and row counts that leave partial blocks."""
+    """Widths other than 2048/8192 (LDS-staged path) and row counts that leave partial blocks; 20483 rows of 2048
+    give the waves uneven row ranges of several passes each."""
     if epilogue == "swiglu" and rows % 2:
         rows += 1
     _check_matvec(wtype, epilogue, 1, 4, rows, cols, seed=rows + 3 * cols)
+
+
+def test_stream_read_timed_hook():
+    """The bandwidth kernel on a device buffer through its timed hook: every launch shape records both events, and the
+    sink (written only for one XOR-folded word that a zero buffer never gives) stays untouched."""
+    import torch
+    buf = torch.zeros(8 << 20, dtype=torch.uint8, device="cuda")
+    sink = torch.zeros(16 * 1024, dtype=torch.int32, device="cuda")
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    stream = torch.cuda.current_stream()
+    a.record(stream)
+    b.record(stream)
+    for bpc in (4, 8, 16):
+        E.launch_stream_read_timed(buf.data_ptr(), buf.numel(), bpc, sink.data_ptr(), sink.numel(), stream.cuda_stream,
+                                   a.cuda_event, b.cuda_event)
+        b.synchronize()
+        assert 0 < a.elapsed_time(b) < 100
+    assert int(sink.abs().sum()) == 0
 
 
 def test_matvec_config1_int8_known_case():
