@@ -19,7 +19,8 @@ per token), timed live with HIP events recorded on the engine's stream around th
 with bytes per launch = weight bytes + the KV bytes the step reads, and ``traffic`` from the
 committed rocprofv3 counter summary (profiles/hbm_traffic.json); ``matvec_roofline`` is the
 standalone fused RMSNorm + gate_up + SwiGLU matvec over rotating weight copies (> 1 GiB, so the
-256 MB Infinity Cache cannot serve them); ``cpu_baseline`` is the CPU oracle (the reference's
+256 MB Infinity Cache cannot serve them), with each weight type's lm_head and, beside each, the time
+the bandwidth kernel takes to read the same weight bytes; ``cpu_baseline`` is the CPU oracle (the reference's
 algorithm restated, oracle/model.py) timed on this host.
 """
 import argparse
@@ -281,16 +282,16 @@ def main() -> int:
             paths[wd].unlink()
 
     head_wd = "bf16" if "bf16" in dtypes else dtypes[0]
-    dom = bench_matvec(head_wd, "gate_up", 16384, 2048, "swiglu", True, 400)
+    dom = bench_matvec(head_wd, "gate_up", 16384, 2048, "swiglu", True, 400, stream=True)
     dom_gbps = dom["bytes"] / dom["avg_us"] / 1e3
     log(f"[bench] gate_up {head_wd} matvec: kernel {dom['avg_us']:.2f} us, {dom_gbps:.0f} GB/s "
-        f"(wall {dom['wall_us_per_launch']:.2f} us per launch)")
+        f"(wall {dom['wall_us_per_launch']:.2f} us per launch; a plain read of its weights {dom['stream_us']:.2f} us)")
     matvecs = []
     if not args.no_kernels:
         for wd in dtypes:
             per = {}
             for name, rows, cols, ep, norm in SHAPES:
-                r = bench_matvec(wd, name, rows, cols, ep, norm, 200 if name != "lm_head" else 50)
+                r = bench_matvec(wd, name, rows, cols, ep, norm, 200 if name != "lm_head" else 50, stream=True)
                 matvecs.append(r)
                 per[name] = r["avg_us"]
             weighted = weighted_us(per)
@@ -340,8 +341,15 @@ def main() -> int:
                             "achieved": round(dom_gbps, 1), "frac": round(dom["frac_of_8tbs"], 4),
                             "frac_of_measured_peak": round(dom_gbps / pk, 4) if pk else None,
                             "bytes_per_launch": dom["bytes"], "avg_us": round(dom["avg_us"], 3),
+                            "stream_read_us": round(dom["stream_us"], 3),
+                            "frac_of_stream_read": round(dom["frac_of_stream"], 4),
+                            "lm_head": {r["wtype"]: {"avg_us": round(r["avg_us"], 3), "frac": round(r["frac_of_8tbs"], 4),
+                                                     "stream_read_us": round(r["stream_us"], 3),
+                                                     "frac_of_stream_read": round(r["frac_of_stream"], 4)}
+                                        for r in matvecs if r.get("name") == "lm_head"},
                             "timing": "mean kernel duration from dispatch-recorded start/end events, "
-                                      "rotating over > 1.5 GiB of weight copies"},
+                                      "rotating over > 1.5 GiB of weight copies; stream_read_us: the bandwidth "
+                                      "kernel reading the same weight bytes on the same copies"},
         "cpu_baseline": cpu,
         "decode": {wd: {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
                    for wd, r in decode.items()},

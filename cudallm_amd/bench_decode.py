@@ -3,6 +3,7 @@ src/tools/cudallm_bench.cpp:41-125), driven through this library's C ABI.
 
     python -m cudallm_amd.bench_decode --suite {ablation,quant,context,tg,long,all} [--names A0_naive,...]
                                         [--model-dir DIR] [--out DIR]
+    python -m cudallm_amd.bench_decode --table DIR      # the runs saved by --out DIR, as a markdown table
 
 Each run decodes `prompt_len` prompt tokens (the reference's prompt: 128000, then (i*7919) % 120000 + 1000),
 then times `gen` greedy steps with the device drained on both sides, `warmup` + `reps` times; the record
@@ -90,13 +91,42 @@ def bench(path, prompt_len: int, gen: int, reps: int, warmup: int = 1, matvec: s
             "gpu_name": torch.cuda.get_device_name(0), "pct_of_peak": 100.0 * gbps / PEAK_GBPS}
 
 
+def markdown_table(out_dir: Path) -> str:
+    """The runs saved under out_dir (--out) as one markdown table in suite order, then the context-scaling ratios
+    (long_*_8000 against tg_* of the same weight type, ctx_opt_4000 against ctx_opt_128) where both runs are there."""
+    recs = {}
+    for suite in SUITES:
+        for name, *_ in SUITES[suite]:
+            f = out_dir / suite / f"{name}.json"
+            if f.exists():
+                recs[name] = (suite, json.loads(f.read_text()))
+    lines = ["| suite | run | weights | options | prompt | gen | tok/s | ms/token | GB/s | % of 8 TB/s |",
+             "|---|---|---|---|---|---|---|---|---|---|"]
+    for name, (suite, r) in recs.items():
+        o = r["options"]
+        lines.append(f"| {suite} | {name} | {r['weight_dtype']} | {o['matvec']}/{o['attn']} fuse={o['fuse']} "
+                     f"graph={o['graph']} | {r['prompt_len']} | {r['gen']} | {r['decode_tok_s_median']:.1f} | "
+                     f"{r['ms_per_token_median']:.3f} | {r['achieved_gbps_median']:.0f} | {r['pct_of_peak']:.1f} |")
+    tok = {n: r["decode_tok_s_median"] for n, (_, r) in recs.items()}
+    ratios = [(f"long_{w}_8000", f"tg_{w}") for w in ("bf16", "int8", "int4")] + [("ctx_opt_4000", "ctx_opt_128")]
+    notes = [f"* {a}: {tok[a]:.1f} tok/s, {100 * (1 - tok[a] / tok[b]):.1f} % below {b} ({tok[b]:.1f})"
+             for a, b in ratios if a in tok and b in tok]
+    return "\n".join(lines) + ("\n\n" + "\n".join(notes) if notes else "") + "\n"
+
+
 def main() -> None:
     ap = argparse.ArgumentParser(description="cudallm decode benchmark suites")
-    ap.add_argument("--suite", choices=(*SUITES, "all"), required=True)
+    ap.add_argument("--suite", choices=(*SUITES, "all"))
+    ap.add_argument("--table", metavar="DIR", help="print the runs saved under DIR (an earlier --out) as markdown")
     ap.add_argument("--names", default="", help="comma-separated subset of run names (default: the whole suite)")
     ap.add_argument("--model-dir", default="/dev/shm/cudallm_models")
     ap.add_argument("--out", default="", help="directory for one JSON file per run (suite/name.json)")
     args = ap.parse_args()
+    if args.table:
+        print(markdown_table(Path(args.table)), end="")
+        return
+    if not args.suite:
+        ap.error("--suite is required (or --table DIR)")
     wanted = {n for n in args.names.split(",") if n}
     suites = list(SUITES) if args.suite == "all" else [args.suite]
     known = {e[0] for s in suites for e in SUITES[s]}

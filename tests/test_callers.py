@@ -275,3 +275,26 @@ def test_profsum_bench_legs():
     assert leg["decode_timed"]["calls"] == K_ and leg["decode_timed"]["mean_us"] == pytest.approx(65.0)
     assert leg["config5_timed"]["calls"] == 1280 and leg["config5_timed"]["mean_us"] == pytest.approx(67.0)
     assert leg["launches"] == leg["expected_launches"] == len(durs)
+
+
+def test_bench_decode_markdown_table(tmp_path):
+    """--table: saved runs in suite order, and the long-context and ctx-4000 ratios."""
+    import json
+    from cudallm_amd import bench_decode as B
+
+    def save(suite, name, wd, plen, tok):
+        d = tmp_path / suite
+        d.mkdir(exist_ok=True)
+        rec = {"weight_dtype": wd, "options": {"matvec": "opt", "attn": "opt", "fuse": 1, "graph": 1},
+               "prompt_len": plen, "gen": 32, "decode_tok_s_median": tok, "ms_per_token_median": 1e3 / tok,
+               "achieved_gbps_median": 4000.0, "pct_of_peak": 50.0}
+        (d / f"{name}.json").write_text(json.dumps(rec))
+
+    save("long", "long_bf16_8000", "bf16", 8000, 1600.0)
+    save("tg", "tg_bf16", "bf16", 1, 2000.0)
+    save("context", "ctx_opt_128", "bf16", 128, 1850.0)
+    text = B.markdown_table(tmp_path)
+    rows = [l for l in text.splitlines() if l.startswith("| ") and "---" not in l][1:]
+    assert [r.split(" | ")[1] for r in rows] == ["ctx_opt_128", "tg_bf16", "long_bf16_8000"]
+    assert "long_bf16_8000: 1600.0 tok/s, 20.0 % below tg_bf16 (2000.0)" in text
+    assert "ctx_opt_4000" not in text
