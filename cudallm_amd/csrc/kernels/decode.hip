@@ -1451,26 +1451,31 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
             // wave and the first half two, so the second half reaches the attention phase sooner (bf16 -8.7, int8
             // -3.7, int4 -6.5 us per step).
             const int ab = (static_cast<int>(blockIdx.x) + G / 2) % G;
+            // Earlier tokens come from the cache and do not depend on this step.  A task's K/V tile is loaded into
+            // registers before its q arrives: the first task's while the qkv phase is still finishing elsewhere,
+            // each later task's (contexts past 4096, more tasks than workgroups) while the task before it computes.
+            u32x4 kt[kTile], vt[kTile];
+            auto load_tile = [&](int tt) {
+                const int kvh = tt % NKV, t0 = (tt / NKV) * kAttnChunk, n = min(kAttnChunk, ctx - t0);
+                const uint16_t* Kg = p.k_cache + l * layer_cache + static_cast<size_t>(kvh) * p.max_seq * HD;
+                const uint16_t* Vg = p.v_cache + l * layer_cache + static_cast<size_t>(kvh) * p.max_seq * HD;
+#pragma unroll
+                for (int k = 0; k < kTile; ++k) {
+                    const int idx = tid + k * kCT, r = idx / 8, c = idx % 8;
+                    if (r < n && t0 + r < pos) {
+                        kt[k] = load_stream(Kg + static_cast<size_t>(t0 + r) * HD + c * 8);
+                        vt[k] = load_stream(Vg + static_cast<size_t>(t0 + r) * HD + c * 8);
+                    }
+                }
+            };
+            if (ab < T) load_tile(ab);
 #pragma unroll 1
             for (int t = ab; t < T; t += G) {
                 const int kvh = t % NKV, split = t / NKV;
                 const int t0 = split * kAttnChunk, n = min(kAttnChunk, ctx - t0);
                 const bool first = t == ab;
                 stamp_attn(p, l, first, 0);
-                const uint16_t* Kg = p.k_cache + l * layer_cache + static_cast<size_t>(kvh) * p.max_seq * HD;
-                const uint16_t* Vg = p.v_cache + l * layer_cache + static_cast<size_t>(kvh) * p.max_seq * HD;
-                // Earlier tokens come from the cache and do not depend on this step: they go into the LDS
-                // tiles while the qkv phase is still finishing elsewhere.
                 {
-                    u32x4 kt[kTile], vt[kTile];
-#pragma unroll
-                    for (int k = 0; k < kTile; ++k) {
-                        const int idx = tid + k * kCT, r = idx / 8, c = idx % 8;
-                        if (r < n && t0 + r < pos) {
-                            kt[k] = load_stream(Kg + static_cast<size_t>(t0 + r) * HD + c * 8);
-                            vt[k] = load_stream(Vg + static_cast<size_t>(t0 + r) * HD + c * 8);
-                        }
-                    }
                     if ((!kDig || kQkvDig) && first) cwait(sm.bar, ep_in, lbad);  // every wave has read the qkv input (or its digits)
 #pragma unroll
                     for (int k = 0; k < kTile; ++k) {
@@ -1480,6 +1485,7 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
                             Vs[r * 8 + c] = vt[k];
                         }
                     }
+                    if (t + G < T) load_tile(t + G);
                 }
                 // q of the group's 4 heads (thread = head-in-group x dim) and, in the split holding this
                 // token, its k and v, rounded to fp16 exactly as the qkv phase wrote them to the cache.
