@@ -1357,6 +1357,30 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
         uint64_t* tact = p.tact + static_cast<size_t>(l) * INTER;
         uint64_t* txo = p.tx + static_cast<size_t>(l + 1) * H;
 
+        // Attention tasks (kv head, 128-token split) start at workgroup G / 2: at 256 workgroups (MI355X's grid) the
+        // second half has one qkv unit per wave and the first half two, so the second half reaches the attention phase
+        // sooner (bf16 -8.7, int8 -3.7, int4 -6.5 us per step).  Earlier tokens come from the cache and do not depend
+        // on this step, so a task's K/V tile is loaded into registers before its q arrives: the first task's during
+        // this workgroup's qkv rows, each later task's (contexts past 4096, more tasks than workgroups) while the
+        // task before it computes.
+        constexpr int kTile = kAttnChunk * 8 / kCT;  // 16-byte chunks per thread
+        const int T = NKV * nsplit;
+        const int ab = (static_cast<int>(blockIdx.x) + G / 2) % G;
+        u32x4 kt[kTile], vt[kTile];
+        auto load_tile = [&](int tt) {
+            const int kvh = tt % NKV, t0 = (tt / NKV) * kAttnChunk, n = min(kAttnChunk, ctx - t0);
+            const uint16_t* Kg = p.k_cache + l * layer_cache + static_cast<size_t>(kvh) * p.max_seq * HD;
+            const uint16_t* Vg = p.v_cache + l * layer_cache + static_cast<size_t>(kvh) * p.max_seq * HD;
+#pragma unroll
+            for (int k = 0; k < kTile; ++k) {
+                const int idx = tid + k * kCT, r = idx / 8, c = idx % 8;
+                if (r < n && t0 + r < pos) {
+                    kt[k] = load_stream(Kg + static_cast<size_t>(t0 + r) * HD + c * 8);
+                    vt[k] = load_stream(Vg + static_cast<size_t>(t0 + r) * HD + c * 8);
+                }
+            }
+        };
+
         // ---- qkv (+ attn_norm prologue, RoPE, fp16 KV write); unit = RoPE pair (i, i+32) of a head ----
         renew();
         {
@@ -1400,6 +1424,7 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
             ep_in = carrive(sm.bar, ep, wave, lane);  // the attention tiles may now overwrite the input / digit table
             stamp_in(p, l, 0, 1);
             drain();
+            if (ab < T) load_tile(ab);
 #pragma unroll 1
             for (int u = gw; u < kPairs; u += NW) {
                 Row<WT> ra, rb;
@@ -1444,31 +1469,7 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
             float* qs = sm.big + kAttnQ;                               // [4][64]
             uint16_t* Ks16 = reinterpret_cast<uint16_t*>(Ks);
             uint16_t* Vs16 = reinterpret_cast<uint16_t*>(Vs);
-            constexpr int kTile = kAttnChunk * 8 / kCT;               // 16-byte chunks per thread
-            const int T = NKV * nsplit;
             stall_at(p, kStallAttn);
-            // Tasks start at workgroup G / 2: at 256 workgroups (MI355X's grid) the second half has one qkv unit per
-            // wave and the first half two, so the second half reaches the attention phase sooner (bf16 -8.7, int8
-            // -3.7, int4 -6.5 us per step).
-            const int ab = (static_cast<int>(blockIdx.x) + G / 2) % G;
-            // Earlier tokens come from the cache and do not depend on this step.  A task's K/V tile is loaded into
-            // registers before its q arrives: the first task's while the qkv phase is still finishing elsewhere,
-            // each later task's (contexts past 4096, more tasks than workgroups) while the task before it computes.
-            u32x4 kt[kTile], vt[kTile];
-            auto load_tile = [&](int tt) {
-                const int kvh = tt % NKV, t0 = (tt / NKV) * kAttnChunk, n = min(kAttnChunk, ctx - t0);
-                const uint16_t* Kg = p.k_cache + l * layer_cache + static_cast<size_t>(kvh) * p.max_seq * HD;
-                const uint16_t* Vg = p.v_cache + l * layer_cache + static_cast<size_t>(kvh) * p.max_seq * HD;
-#pragma unroll
-                for (int k = 0; k < kTile; ++k) {
-                    const int idx = tid + k * kCT, r = idx / 8, c = idx % 8;
-                    if (r < n && t0 + r < pos) {
-                        kt[k] = load_stream(Kg + static_cast<size_t>(t0 + r) * HD + c * 8);
-                        vt[k] = load_stream(Vg + static_cast<size_t>(t0 + r) * HD + c * 8);
-                    }
-                }
-            };
-            if (ab < T) load_tile(ab);
 #pragma unroll 1
             for (int t = ab; t < T; t += G) {
                 const int kvh = t % NKV, split = t / NKV;
