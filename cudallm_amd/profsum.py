@@ -112,7 +112,14 @@ def bench_legs(rows, steps: int, warmup: int, prompt: int = 16, c5_reps: int = 5
     out = {}
     for wd, us in per.items():
         t0 = prompt + warmup + prompt
-        leg = {"decode_timed": _stats(us[t0:t0 + steps])}
+        timed = us[t0:t0 + steps]
+        leg = {"decode_timed": _stats(timed)}
+        # The timed steps by attention split count: step i attends over prompt + 1 + i positions, in 128-token splits.
+        by = {}
+        for i, v in enumerate(timed):
+            by.setdefault((prompt + 1 + i + 127) // 128, []).append((prompt + 1 + i, v))
+        leg["decode_timed_by_splits"] = {f"{k} ({c[0][0]}..{c[-1][0]})": _stats([v for _, v in c])
+                                         for k, c in sorted(by.items())}
         c0 = t0 + steps + 1
         c5 = []
         for r in range(c5_warmup, c5_warmup + c5_reps):
