@@ -319,6 +319,41 @@ def test_largest_max_seq_matches_multikernel(wd, model_dir, gpu):
         ref.close()
 
 
+def test_context_past_16384_matches_multikernel(model_dir, gpu):
+    """Past 128 splits (three 64-split blocks in the long merge) on the persistent kernel at max_seq_len 32768, int8
+    (its KV rows written in the qkv phase), against the multi-kernel path teacher-forced to position 17000."""
+    from cudallm_amd import synth
+    wd, steps = "int8", 17000
+    path = model_dir / f"synth_seed7_{wd}_ms131072.cudallm"
+    if not path.exists():
+        synth.write_model(path, wd, seed=7, max_seq_len=131072)
+    os.environ["CUDALLM_PERSISTENT"] = "0"
+    try:
+        ref = E.Engine(path, max_seq_len=32768)
+    finally:
+        del os.environ["CUDALLM_PERSISTENT"]
+    eng = E.Engine(path, max_seq_len=32768)
+    try:
+        assert ref.step_kind[0] == "program"
+        _persistent(eng)
+        toks, worst, agree, checked = [128000], 0.0, 0, 0
+        for i in range(steps):
+            check = i in (8191, 16383, 16384, 16385, 16511, 16512, 16999)
+            n_ref, lg_ref = ref.step(toks[-1], want_logits=check)
+            n_eng, lg_eng = eng.step(toks[-1], want_logits=check)
+            if check:
+                worst = max(worst, float(np.abs(lg_eng - lg_ref).max()) / float(np.abs(lg_ref).max()))
+                agree += int(n_eng == n_ref)
+                checked += 1
+            toks.append(n_ref)
+        print(f"[engine] {wd} persistent vs multi-kernel to ctx {steps} (max_seq 32768): worst rel logit diff "
+              f"{worst:.2e}, argmax agree {agree}/{checked}", flush=True)
+        assert worst < 2e-3 and agree >= checked - 1
+    finally:
+        eng.close()
+        ref.close()
+
+
 def test_trace_needs_the_persistent_kernel(model_path):
     with E.Engine(model_path("int4"), fuse=False, max_seq_len=256) as eng:
         with pytest.raises(E.CudaLLMError) as ei:
