@@ -60,6 +60,52 @@ __device__ __forceinline__ void store_out(float* y, int r, float d, float du) {
     }
 }
 
+// x of lane l ^ M (M a power of two below 64): quad permutes for 1 and 2, a rotation by 8 inside each 16-lane row
+// for 8 (the same lanes), the LDS crossbar's swizzle (bit mode, 32-lane groups) for 4 and 16, a permute for 32.
+template <int M>
+__device__ __forceinline__ float xor_lanes(float x) {
+    if constexpr (M == 1) return dpp<kDppXor1>(x);
+    if constexpr (M == 2) return dpp<kDppXor2>(x);
+    if constexpr (M == 8) return dpp<0x128>(x);  // row_ror:8
+    if constexpr (M == 4 || M == 16)
+        return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, x), 0x1F | (M << 10)));
+    if constexpr (M == 32) return __shfl_xor(x, 32);
+}
+
+// Sums R per-lane partials (one per row; R = 1, 2, 4 or 8) over the wave: lane l ends with the sum of row l mod R.
+// log2 R exchange steps halve the values a lane holds (bit b of the lane picks the half it keeps; the other half goes
+// to lane l ^ 2^b, which keeps it), then the remaining lane bits are summed directly.  About 3 instructions per
+// row instead of a full reduction (4 row operations, 4 readlanes, 3 adds) per row.
+template <int R, int B = 0>
+__device__ __forceinline__ void exchange(float (&v)[R], int lane) {
+    if constexpr ((1 << B) < R) {
+        constexpr int M = 1 << B;
+        const bool hi = (lane & M) != 0;
+#pragma unroll
+        for (int k = 0; k < R / (2 << B); ++k) {
+            const float a = v[2 * k], c = v[2 * k + 1];
+            v[k] = (hi ? c : a) + xor_lanes<M>(hi ? a : c);
+        }
+        exchange<R, B + 1>(v, lane);
+    }
+}
+template <int R>
+__device__ __forceinline__ float rows_sum(const float (&d)[R], int lane) {
+    static_assert(R == 1 || R == 2 || R == 4 || R == 8, "rows per pass");
+    float v[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i) v[i] = d[i];
+    exchange<R>(v, lane);
+    float x = v[0];
+    if constexpr (R < 2) x += xor_lanes<1>(x);
+    if constexpr (R < 4) x += xor_lanes<2>(x);
+    if constexpr (R < 8) x += xor_lanes<4>(x);
+    x += xor_lanes<8>(x);
+    x += xor_lanes<16>(x);
+    x += xor_lanes<32>(x);
+    return x;
+}
+
 template <WType WT, Epilogue EP, bool NORM, int KS, int R>
 __global__ void __launch_bounds__(kThreads) matvec_fast(MatvecArgs a) {
     using F = Fmt<WT>;
@@ -231,9 +277,9 @@ __global__ void __launch_bounds__(kThreads) matvec_fast(MatvecArgs a) {
                         return fmaf(static_cast<float>(p2), 65536.f, static_cast<float>(p0 + 256 * p1)) * half_bits_to_float(g);
                     }
                 };
-                d[i] = wave_sum(dot(b.v[i], b.g[i])) * dsc;
+                d[i] = dot(b.v[i], b.g[i]);
                 du[i] = 0.f;
-                if constexpr (GLU) du[i] = wave_sum(dot(b.vu[i], b.gu[i])) * dsc;
+                if constexpr (GLU) du[i] = dot(b.vu[i], b.gu[i]);
             } else {
                 float s = 0.f, su = 0.f;
 #pragma unroll
@@ -249,32 +295,46 @@ __global__ void __launch_bounds__(kThreads) matvec_fast(MatvecArgs a) {
                     s = half_bits_to_float(b.g[i]) * (s - 8.f * xsum);
                     if constexpr (GLU) su = half_bits_to_float(b.gu[i]) * (su - 8.f * xsum);
                 }
-                d[i] = wave_sum(s);
-                du[i] = GLU ? wave_sum(su) : 0.f;
+                d[i] = s;
+                du[i] = su;
             }
+        }
+        // Lane l: the sums of row r0 + (l mod R) (times 2^-e for the digit dots).  int4's 2048-wide rows (1 KiB, the
+        // most rows per byte) reduce all R rows at once (rows_sum: int4 lm_head 28.2 -> 26.2 us, gate_up 8.0 -> 7.3 us
+        // on MI355X); the other forms keep a full reduction per row, which measured as fast or faster for them (bf16
+        // down 7.3 against 8.4 us).
+        float tot = 0.f, tot_u = 0.f;
+        if constexpr (WT == WType::INT4 && KS == 1) {
+            tot = rows_sum<R>(d, lane);
+            if constexpr (GLU) tot_u = rows_sum<R>(du, lane);
+        } else {
+#pragma unroll
+            for (int i = 0; i < R; ++i) {
+                const float si = wave_sum(d[i]);
+                const float sui = GLU ? wave_sum(du[i]) : 0.f;
+                if (lane % R == i) {
+                    tot = si;
+                    tot_u = sui;
+                }
+            }
+        }
+        if constexpr (DIG) {
+            tot *= dsc;
+            tot_u *= dsc;
         }
 
         if constexpr (KS == 1) {
-            // Lane held + i keeps row r0 + i until the wave's last pass (no store inside the loop).
-#pragma unroll
-            for (int i = 0; i < R; ++i) {
-                if (lane == held + i) {
-                    acc = d[i];
-                    acc_u = du[i];
-                    acc_row = r0 + i;
-                }
+            // Lane held + i keeps row r0 + i until the wave's last pass (no store inside the loop); held is a multiple
+            // of R, so that lane already holds row i's sum.
+            if (lane >= held && lane < held + R) {
+                acc = tot;
+                acc_u = tot_u;
+                acc_row = r0 + lane - held;
             }
             held += R;
         } else {
             // Lane i (< R) holds row r0 + i.
-            float mine = d[0], mine_u = du[0];
-#pragma unroll
-            for (int i = 1; i < R; ++i) {
-                if (lane == i) {
-                    mine = d[i];
-                    mine_u = du[i];
-                }
-            }
+            const float mine = tot, mine_u = tot_u;
             if (lane < R) {
                 const int slot = (slice * ROWS_WG + grp * R + lane) * NP;
                 part[slot] = mine;
