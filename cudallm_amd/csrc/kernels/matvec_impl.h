@@ -119,7 +119,9 @@ __global__ void __launch_bounds__(kThreads) matvec_fast(MatvecArgs a) {
     __shared__ float part[KS > 1 ? KS * ROWS_WG * NP : 1];
 
     const int tid = threadIdx.x;
-    const int wave = tid / kWave, lane = tid % kWave;
+    // The wave index through readfirstlane: the compiler then knows it is uniform, so every row index and weight
+    // address derived from it is computed once per wave in scalar registers instead of in every lane.
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave), lane = tid % kWave;
     const int slice = wave % KS, grp = wave / KS;
     const int out_rows = GLU ? a.rows / 2 : a.rows;
     // Row blocks are dealt to the workgroups in turn; base is the same for every wave of a workgroup, so the
