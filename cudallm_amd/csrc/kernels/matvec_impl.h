@@ -145,10 +145,14 @@ __global__ void __launch_bounds__(kThreads) matvec_fast(MatvecArgs a) {
         }
     }
     const size_t rb = row_bytes<WT>(a.cols);
-    const char* wl = static_cast<const char*>(a.w) + static_cast<size_t>(slice) * (kSlice * 16 / F::CPC) + lane * 16;
+    // Addresses are a row base that is uniform across the wave (scalar registers) plus a 32-bit lane offset, the
+    // form of a load with a scalar base: one offset register per lane instead of a 64-bit address per row.
+    const char* wbase = static_cast<const char*>(a.w);
+    const uint32_t woff = static_cast<uint32_t>(slice * (kSlice * 16 / F::CPC) + lane * 16);
     const int groups_per_row = a.cols / 128;
     // int4: one 128-column group per lane; lanes 4g..4g+3 share scale g of the slice.
-    const uint16_t* gsc = static_cast<const uint16_t*>(a.scales) + slice * (kSlice / 128) + lane / 4;
+    const uint16_t* sbase = static_cast<const uint16_t*>(a.scales);
+    const uint32_t soff = static_cast<uint32_t>(slice * (kSlice / 128) + lane / 4);
 
     // The R rows of one pass: weight chunks and, for int4, the lane's group scales.  Two of these alternate, so the
     // next pass's loads are in flight while this pass is multiplied.
@@ -163,14 +167,16 @@ __global__ void __launch_bounds__(kThreads) matvec_fast(MatvecArgs a) {
 #pragma unroll
         for (int i = 0; i < R; ++i) {
             const int rc = min(r0 + i, out_rows - 1);
+            const char* row = wbase + static_cast<size_t>(rc) * rb;
+            const char* row_u = wbase + static_cast<size_t>(rc + out_rows) * rb;
 #pragma unroll
             for (int k = 0; k < F::CPL; ++k) {
-                b.v[i][k] = load_stream(wl + static_cast<size_t>(rc) * rb + k * 1024);
-                if constexpr (GLU) b.vu[i][k] = load_stream(wl + static_cast<size_t>(rc + out_rows) * rb + k * 1024);
+                b.v[i][k] = load_stream(row + woff + k * 1024);
+                if constexpr (GLU) b.vu[i][k] = load_stream(row_u + woff + k * 1024);
             }
             if constexpr (WT == WType::INT4) {
-                b.g[i] = gsc[static_cast<size_t>(rc) * groups_per_row];
-                if constexpr (GLU) b.gu[i] = gsc[static_cast<size_t>(rc + out_rows) * groups_per_row];
+                b.g[i] = gload(sbase + static_cast<size_t>(rc) * groups_per_row + soff);
+                if constexpr (GLU) b.gu[i] = gload(sbase + static_cast<size_t>(rc + out_rows) * groups_per_row + soff);
             }
         }
     };

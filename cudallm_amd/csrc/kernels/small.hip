@@ -27,12 +27,12 @@ int device_cu_count() {
 
 // The library's rpb when the caller passes 0, per weight type and shape class, from an rpb sweep of the standalone
 // matvec on MI355X (each class's fastest mean kernel time; e.g. bf16 gate_up 12.97 -> 12.30 us at rpb 1, bf16 down
-// 8.21 -> 7.51 us at rpb 8).  Classes: 0 other, 1 SwiGLU (gate_up), 2 8192 columns (down), 3 vocabulary-sized
-// (>= 65536 rows: lm_head).
+// 8.21 -> 7.51 us and int4 down 6.6 -> 5.2 us at rpb 8).  Classes: 0 other, 1 SwiGLU (gate_up), 2 8192 columns
+// (down), 3 vocabulary-sized (>= 65536 rows: lm_head).
 constexpr int kDefaultRpb[3][4] = {
     {2, 1, 8, 2},  // bf16
     {4, 4, 4, 4},  // int8
-    {4, 8, 4, 8},  // int4
+    {4, 8, 8, 8},  // int4
 };
 
 int default_rpb(WType wt, Epilogue ep, int rows, int cols) {

@@ -26,7 +26,7 @@ SHAPES = [("qkv", 3072, 2048, "store", True), ("wo", 2048, 2048, "add", False),
 RPBS = (1, 2, 4, 8)
 # The library's choice when rpb = 0 (kDefaultRpb / default_rpb in csrc/kernels/small.hip), per weight type and shape
 # class: other, SwiGLU, 8192 columns, >= 65536 rows.
-DEFAULT_RPB = {"bf16": (2, 1, 8, 2), "int8": (4, 4, 4, 4), "int4": (4, 8, 4, 8)}
+DEFAULT_RPB = {"bf16": (2, 1, 8, 2), "int8": (4, 4, 4, 4), "int4": (4, 8, 8, 8)}
 
 
 def default_rpb(wd: str, ep: str, rows: int, cols: int) -> int:

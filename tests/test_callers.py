@@ -157,7 +157,7 @@ def test_default_rpb_matches_the_library():
     assert got == K.DEFAULT_RPB
     assert "ep == Epilogue::SWIGLU ? 1 : cols >= 8192 ? 2 : rows >= 65536 ? 3 : 0" in body
     assert [K.default_rpb("bf16", ep, r, c) for _, r, c, ep, _ in K.SHAPES] == [2, 2, 1, 8, 2]
-    assert [K.default_rpb("int4", ep, r, c) for _, r, c, ep, _ in K.SHAPES] == [4, 4, 8, 4, 8]
+    assert [K.default_rpb("int4", ep, r, c) for _, r, c, ep, _ in K.SHAPES] == [4, 4, 8, 8, 8]
 
 
 def test_shape_winners():
