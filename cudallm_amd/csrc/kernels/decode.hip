@@ -744,11 +744,10 @@ __device__ __forceinline__ float row_dot(const Row<WT>& r, const float* xr, floa
     return s;
 }
 
-// Complete dot of a 2048-wide quantised row against the input digits, uniform across the wave;
-// `sc` = 2^-e.  int8: sum_k 256^k sum(q d_k), times the row scale; int4: sum_k 16^k sum(q d_k) per lane
-// (the stored nibble u = q + 8 becomes q by xor 8), times the lane's group scale.
+// A lane's share of the dot of a 2048-wide quantised row with the input digits, before any scale: int8:
+// sum_k 256^k sum(q d_k); int4: sum_k 16^k sum(q d_k) (the stored nibble u = q + 8 becomes q by xor 8).
 template <WType WT>
-__device__ __forceinline__ float row_dot_dig(const Row<WT>& r, const Dig<WT>& dg, float sc) {
+__device__ __forceinline__ float dig_part(const Row<WT>& r, const Dig<WT>& dg) {
     if constexpr (WT == WType::INT8) {
         int a0 = 0, a1 = 0, a2 = 0;
 #pragma unroll
@@ -760,9 +759,7 @@ __device__ __forceinline__ float row_dot_dig(const Row<WT>& r, const Dig<WT>& dg
                 a1 = __builtin_amdgcn_sdot4(w, static_cast<int>(dg.d[(1 * 2 + c) * 4 + i]), a1, false);
                 a2 = __builtin_amdgcn_sdot4(w, static_cast<int>(dg.d[(2 * 2 + c) * 4 + i]), a2, false);
             }
-        float t = fmaf(fmaf(static_cast<float>(a2), 256.f, static_cast<float>(a1)), 256.f, static_cast<float>(a0));
-        t = wave_sum(t);
-        return t * sc * r.s;
+        return fmaf(fmaf(static_cast<float>(a2), 256.f, static_cast<float>(a1)), 256.f, static_cast<float>(a0));
     } else {
         int a[6] = {0, 0, 0, 0, 0, 0};
 #pragma unroll
@@ -772,10 +769,26 @@ __device__ __forceinline__ float row_dot_dig(const Row<WT>& r, const Dig<WT>& dg
             for (int k = 0; k < 6; ++k) a[k] = __builtin_amdgcn_sdot8(w, static_cast<int>(dg.d[k * 4 + i]), a[k], false);
         }
         const int p0 = a[0] + 16 * a[1], p1 = a[2] + 16 * a[3], p2 = a[4] + 16 * a[5];
-        float t = fmaf(static_cast<float>(p2), 65536.f, static_cast<float>(p0 + 256 * p1));
-        t = wave_sum(t * r.s);
-        return t * sc;
+        return fmaf(static_cast<float>(p2), 65536.f, static_cast<float>(p0 + 256 * p1));
     }
+}
+
+// Complete dot of a 2048-wide quantised row against the input digits, uniform across the wave; `sc` = 2^-e.
+// int8 scales the wave's sum by the row scale, int4 each lane's share by its group scale.
+template <WType WT>
+__device__ __forceinline__ float row_dot_dig(const Row<WT>& r, const Dig<WT>& dg, float sc) {
+    if constexpr (WT == WType::INT8) {
+        return wave_sum(dig_part<WT>(r, dg)) * sc * r.s;
+    } else {
+        return wave_sum(dig_part<WT>(r, dg) * r.s) * sc;
+    }
+}
+
+// A lane's share of row_dot_dig, scaled by the row's (int8) or the lane's group (int4) scale but not yet summed
+// over the wave: lm_head sums its rows together with rows_sum.
+template <WType WT>
+__device__ __forceinline__ float row_part_dig(const Row<WT>& r, const Dig<WT>& dg) {
+    return dig_part<WT>(r, dg) * r.s;
 }
 
 // ---- int4 down projection on digits ------------------------------------------------------------
@@ -1868,25 +1881,37 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
             for (int i = 0; i < kLmR<WT>; ++i) take_row<WT>(sm, cs, wave, lane, lbad, rr[i]);
             release_early<WT>(sm, cs, wave, lane);
             float d[kLmR<WT>];
+            if constexpr (kDig) {
+                // The unit's rows are summed together: lane l ends with row l mod kLmR, which is the logit it
+                // stores (lane nrow + i holds row i) and the only row it compares for the argmax.
 #pragma unroll
-            for (int i = 0; i < kLmR<WT>; ++i) {
-                if constexpr (kDig) {
-                    d[i] = row_dot_dig<WT>(rr[i], dg, dsc);
-                } else {
-                    d[i] = row_dot<WT>(rr[i], xr, xsum);
-                }
-            }
-            release_late<WT>(sm, cs, wave, lane);
-#pragma unroll
-            for (int i = 0; i < kLmR<WT>; ++i) {
-                const int r = u * kLmR<WT> + i;
-                if (lane == nrow + i) {
-                    lg = d[i];
+                for (int i = 0; i < kLmR<WT>; ++i) d[i] = row_part_dig<WT>(rr[i], dg);
+                release_late<WT>(sm, cs, wave, lane);
+                const float x = rows_sum<kLmR<WT>>(d, lane) * dsc;
+                const int r = u * kLmR<WT> + lane % kLmR<WT>;
+                if (lane / kLmR<WT> == nrow / kLmR<WT>) {
+                    lg = x;
                     lr = r;
                 }
-                if (arg_better(d[i], r, bv, bi)) {
-                    bv = d[i];
+                if (arg_better(x, r, bv, bi)) {
+                    bv = x;
                     bi = r;
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < kLmR<WT>; ++i) d[i] = row_dot<WT>(rr[i], xr, xsum);
+                release_late<WT>(sm, cs, wave, lane);
+#pragma unroll
+                for (int i = 0; i < kLmR<WT>; ++i) {
+                    const int r = u * kLmR<WT> + i;
+                    if (lane == nrow + i) {
+                        lg = d[i];
+                        lr = r;
+                    }
+                    if (arg_better(d[i], r, bv, bi)) {
+                        bv = d[i];
+                        bi = r;
+                    }
                 }
             }
             nrow += kLmR<WT>;
@@ -1897,6 +1922,12 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
             }
         }
         if (lane < nrow) *glob(p.logits + lr) = lg;
+        if constexpr (kDig) {  // lanes l and l' hold the same rows when l = l' mod kLmR: reduce over l mod kLmR
+            static_assert(kLmR<WT> <= 8, "the argmax reduction covers up to 8 lanes");
+            if constexpr (kLmR<WT> >= 2) arg_dpp<kDppXor1>(bv, bi);
+            if constexpr (kLmR<WT> >= 4) arg_dpp<kDppXor2>(bv, bi);
+            if constexpr (kLmR<WT> >= 8) arg_dpp<kDppHalfMirror>(bv, bi);
+        }
         if (lane == 0) {
             sm.red_v[wave] = bv;
             sm.red_i[wave] = bi;

@@ -60,52 +60,6 @@ __device__ __forceinline__ void store_out(float* y, int r, float d, float du) {
     }
 }
 
-// x of lane l ^ M (M a power of two below 64): quad permutes for 1 and 2, a rotation by 8 inside each 16-lane row
-// for 8 (the same lanes), the LDS crossbar's swizzle (bit mode, 32-lane groups) for 4 and 16, a permute for 32.
-template <int M>
-__device__ __forceinline__ float xor_lanes(float x) {
-    if constexpr (M == 1) return dpp<kDppXor1>(x);
-    if constexpr (M == 2) return dpp<kDppXor2>(x);
-    if constexpr (M == 8) return dpp<0x128>(x);  // row_ror:8
-    if constexpr (M == 4 || M == 16)
-        return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, x), 0x1F | (M << 10)));
-    if constexpr (M == 32) return __shfl_xor(x, 32);
-}
-
-// Sums R per-lane partials (one per row; R = 1, 2, 4 or 8) over the wave: lane l ends with the sum of row l mod R.
-// log2 R exchange steps halve the values a lane holds (bit b of the lane picks the half it keeps; the other half goes
-// to lane l ^ 2^b, which keeps it), then the remaining lane bits are summed directly.  About 3 instructions per
-// row instead of a full reduction (4 row operations, 4 readlanes, 3 adds) per row.
-template <int R, int B = 0>
-__device__ __forceinline__ void exchange(float (&v)[R], int lane) {
-    if constexpr ((1 << B) < R) {
-        constexpr int M = 1 << B;
-        const bool hi = (lane & M) != 0;
-#pragma unroll
-        for (int k = 0; k < R / (2 << B); ++k) {
-            const float a = v[2 * k], c = v[2 * k + 1];
-            v[k] = (hi ? c : a) + xor_lanes<M>(hi ? a : c);
-        }
-        exchange<R, B + 1>(v, lane);
-    }
-}
-template <int R>
-__device__ __forceinline__ float rows_sum(const float (&d)[R], int lane) {
-    static_assert(R == 1 || R == 2 || R == 4 || R == 8, "rows per pass");
-    float v[R];
-#pragma unroll
-    for (int i = 0; i < R; ++i) v[i] = d[i];
-    exchange<R>(v, lane);
-    float x = v[0];
-    if constexpr (R < 2) x += xor_lanes<1>(x);
-    if constexpr (R < 4) x += xor_lanes<2>(x);
-    if constexpr (R < 8) x += xor_lanes<4>(x);
-    x += xor_lanes<8>(x);
-    x += xor_lanes<16>(x);
-    x += xor_lanes<32>(x);
-    return x;
-}
-
 template <WType WT, Epilogue EP, bool NORM, int KS, int R>
 __global__ void __launch_bounds__(kThreads) matvec_fast(MatvecArgs a) {
     using F = Fmt<WT>;
