@@ -1269,6 +1269,9 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
     // store per row) instead of 2-byte stores from 32 waves of the qkv phase: int4 -7 us per step on MI355X; bf16 +3
     // and int8 +1 us, so they keep the qkv phase's stores.
     constexpr bool kKvInAttn = WT == WType::INT4;
+    // The quantised kernels score a lane's two tokens in one branch-free loop (int8 -6, int4 -5 us per step with the
+    // P.V reduction below); bf16 keeps one branch per token, which measured 3 us faster for it.
+    constexpr bool kFastScores = WT != WType::BF16;
     __shared__ Smem<WT> sm;
 
     if (threadIdx.x < kCW) {
@@ -1534,23 +1537,44 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
                     f32x4 qv[HD / 4];
 #pragma unroll
                     for (int i = 0; i < HD / 4; ++i) qv[i] = *reinterpret_cast<const f32x4*>(qs + wave * HD + 4 * i);
+                    if constexpr (kFastScores) {
+                        // Both tokens in one loop, without a branch (rows past n hold stale values and are selected
+                        // away below), so the two tokens' FMA chains interleave.
+                        float dd[2][4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-                    for (int k = 0; k < 2; ++k) {
-                        const int j = lane + kWave * k;
-                        if (j < n) {
-                            float dd[4] = {0.f, 0.f, 0.f, 0.f};
+                        for (int i = 0; i < HD / 8; ++i) {
 #pragma unroll
-                            for (int i = 0; i < HD / 8; ++i) {
-                                const u32x4 kk = *reinterpret_cast<const u32x4*>(Ks + j * kKs + 4 * i);
+                            for (int k = 0; k < 2; ++k) {
+                                const u32x4 kk = *reinterpret_cast<const u32x4*>(Ks + (lane + kWave * k) * kKs + 4 * i);
 #pragma unroll
                                 for (int e = 0; e < 4; ++e) {
-                                    dd[e] = fmaf(half_bits_to_float(static_cast<uint16_t>(kk[e])), qv[2 * i + e / 2][2 * (e % 2)], dd[e]);
-                                    dd[e] = fmaf(half_bits_to_float(static_cast<uint16_t>(kk[e] >> 16)), qv[2 * i + e / 2][2 * (e % 2) + 1], dd[e]);
+                                    dd[k][e] = fmaf(half_bits_to_float(static_cast<uint16_t>(kk[e])), qv[2 * i + e / 2][2 * (e % 2)], dd[k][e]);
+                                    dd[k][e] = fmaf(half_bits_to_float(static_cast<uint16_t>(kk[e] >> 16)), qv[2 * i + e / 2][2 * (e % 2) + 1], dd[k][e]);
                                 }
                             }
-                            s[k] = 0.125f * ((dd[0] + dd[1]) + (dd[2] + dd[3]));  // 4 chains: 2.5-5.5 us per step
-                        } else {
-                            s[k] = -INFINITY;
+                        }
+#pragma unroll
+                        for (int k = 0; k < 2; ++k)  // 4 chains per token: 2.5-5.5 us per step
+                            s[k] = lane + kWave * k < n ? 0.125f * ((dd[k][0] + dd[k][1]) + (dd[k][2] + dd[k][3])) : -INFINITY;
+                    } else {
+#pragma unroll
+                        for (int k = 0; k < 2; ++k) {
+                            const int j = lane + kWave * k;
+                            if (j < n) {
+                                float dd[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                                for (int i = 0; i < HD / 8; ++i) {
+                                    const u32x4 kk = *reinterpret_cast<const u32x4*>(Ks + j * kKs + 4 * i);
+#pragma unroll
+                                    for (int e = 0; e < 4; ++e) {
+                                        dd[e] = fmaf(half_bits_to_float(static_cast<uint16_t>(kk[e])), qv[2 * i + e / 2][2 * (e % 2)], dd[e]);
+                                        dd[e] = fmaf(half_bits_to_float(static_cast<uint16_t>(kk[e] >> 16)), qv[2 * i + e / 2][2 * (e % 2) + 1], dd[e]);
+                                    }
+                                }
+                                s[k] = 0.125f * ((dd[0] + dd[1]) + (dd[2] + dd[3]));  // 4 chains: 2.5-5.5 us per step
+                            } else {
+                                s[k] = -INFINITY;
+                            }
                         }
                     }
                 }
@@ -1579,21 +1603,26 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeParams p) {
                         o[2 * e + 1] = fmaf(pj, half_bits_to_float(static_cast<uint16_t>(vv[e] >> 16)), o[2 * e + 1]);
                     }
                 }
+                const int h = kvh * 4 + wave;
+                // The 8 token phases summed across lanes: within each 16-lane row by DPP, across rows by the
+                // permlane swaps (lanes l and l ^ 16, then l and l ^ 32), without a trip through the LDS unit.
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                     o[e] += dpp<kDppRor8>(o[e]);
-                    o[e] += __shfl_xor(o[e], 16);
-                    o[e] += __shfl_xor(o[e], 32);
+                    o[e] = sum_lanes_xor<16>(o[e]);
+                    o[e] = sum_lanes_xor<32>(o[e]);
                 }
-                const int h = kvh * 4 + wave;
-                // Every lane holds its column group's 8 sums; lane j takes column j (element j % 8 of group j / 8,
-                // from lane j / 8), so the wave writes its 64 outputs with one store: whole 64-byte lines.
-                float oj = 0.f;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const float t = __shfl(o[e], lane >> 3);
-                    if ((lane & 7) == e) oj = t;
+                // Every lane holds its column group's 8 sums; lane j takes column j (element j % 8 of group j / 8)
+                // through the wave's q slot in LDS (its q is in registers), so the wave writes its 64 outputs with
+                // one store: whole 64-byte lines.
+                float* ot = qs + wave * HD;
+                if (lane < 8) {
+                    *reinterpret_cast<f32x4*>(ot + 8 * lane) = f32x4{o[0], o[1], o[2], o[3]};
+                    *reinterpret_cast<f32x4*>(ot + 8 * lane + 4) = f32x4{o[4], o[5], o[6], o[7]};
                 }
+                __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                const float oj = ot[lane];
                 if (nsplit == 1) {
                     tstore(tatt + h * HD + lane, oj * (1.f / lsum), tg + T_ATT);
                 } else {

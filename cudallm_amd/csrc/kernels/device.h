@@ -110,6 +110,23 @@ __device__ __forceinline__ float rows_sum(const float (&d)[R], int lane) {
     return x;
 }
 
+// x of lane l plus x of lane l ^ M, for M = 16 or 32, by gfx950's permlane swaps (VALU, no LDS).  With x in both
+// registers, v_permlane16_swap exchanges the odd 16-lane rows of the first with the even rows of the second (the
+// 32-lane form: the upper half of the first with the lower half of the second), so each register ends with one lane
+// of every pair (l, l ^ M) and their sum is the pair's sum in both lanes.  Inline asm because the compiler's builtin
+// returns the first register for both results; the s_nop covers the wait states after the VALU writes of x.
+template <int M>
+__device__ __forceinline__ float sum_lanes_xor(float x) {
+    static_assert(M == 16 || M == 32, "row swaps");
+    unsigned a = __builtin_bit_cast(unsigned, x), b = a;
+    if constexpr (M == 16) {
+        asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    } else {
+        asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    }
+    return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+}
+
 // Block-wide sum for blockDim.x a multiple of 64 (<= 1024); `scratch` holds 16 floats.
 __device__ __forceinline__ float block_sum(float v, float* scratch) {
     v = wave_sum(v);
