@@ -64,6 +64,23 @@ __device__ __forceinline__ float wave_max(float v) {
     return fmaxf(fmaxf(a, b), fmaxf(c, d));
 }
 
+// x of lane l plus x of lane l ^ M, for M = 16 or 32, by gfx950's permlane swaps (VALU, no LDS).  With x in both
+// registers, v_permlane16_swap exchanges the odd 16-lane rows of the first with the even rows of the second (the
+// 32-lane form: the upper half of the first with the lower half of the second), so each register ends with one lane
+// of every pair (l, l ^ M) and their sum is the pair's sum in both lanes.  Inline asm because the compiler's builtin
+// returns the first register for both results; the s_nop covers the wait states after the VALU writes of x.
+template <int M>
+__device__ __forceinline__ float sum_lanes_xor(float x) {
+    static_assert(M == 16 || M == 32, "row swaps");
+    unsigned a = __builtin_bit_cast(unsigned, x), b = a;
+    if constexpr (M == 16) {
+        asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    } else {
+        asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    }
+    return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+}
+
 // x of lane l ^ M (M a power of two below 64): quad permutes for 1 and 2, a rotation by 8 inside each 16-lane row
 // for 8 (the same lanes), the LDS crossbar's swizzle (bit mode, 32-lane groups) for 4 and 16, a permute for 32.
 template <int M>
@@ -79,7 +96,8 @@ __device__ __forceinline__ float xor_lanes(float x) {
 // Sums R per-lane partials (one per row; R = 1, 2, 4 or 8) over the wave: lane l ends with the sum of row l mod R.
 // log2 R exchange steps halve the values a lane holds (bit b of the lane picks the half it keeps; the other half goes
 // to lane l ^ 2^b, which keeps it), then the remaining lane bits are summed directly.  About 3 instructions per
-// row instead of a full reduction (4 row operations, 4 readlanes, 3 adds) per row.
+// row instead of a full reduction (4 row operations, 4 readlanes, 3 adds) per row.  The last two steps are the
+// permlane swaps (sum_lanes_xor).
 template <int R, int B = 0>
 __device__ __forceinline__ void exchange(float (&v)[R], int lane) {
     if constexpr ((1 << B) < R) {
@@ -105,26 +123,8 @@ __device__ __forceinline__ float rows_sum(const float (&d)[R], int lane) {
     if constexpr (R < 4) x += xor_lanes<2>(x);
     if constexpr (R < 8) x += xor_lanes<4>(x);
     x += xor_lanes<8>(x);
-    x += xor_lanes<16>(x);
-    x += xor_lanes<32>(x);
-    return x;
-}
-
-// x of lane l plus x of lane l ^ M, for M = 16 or 32, by gfx950's permlane swaps (VALU, no LDS).  With x in both
-// registers, v_permlane16_swap exchanges the odd 16-lane rows of the first with the even rows of the second (the
-// 32-lane form: the upper half of the first with the lower half of the second), so each register ends with one lane
-// of every pair (l, l ^ M) and their sum is the pair's sum in both lanes.  Inline asm because the compiler's builtin
-// returns the first register for both results; the s_nop covers the wait states after the VALU writes of x.
-template <int M>
-__device__ __forceinline__ float sum_lanes_xor(float x) {
-    static_assert(M == 16 || M == 32, "row swaps");
-    unsigned a = __builtin_bit_cast(unsigned, x), b = a;
-    if constexpr (M == 16) {
-        asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-    } else {
-        asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-    }
-    return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+    x = sum_lanes_xor<16>(x);
+    return sum_lanes_xor<32>(x);
 }
 
 // Block-wide sum for blockDim.x a multiple of 64 (<= 1024); `scratch` holds 16 floats.
