@@ -25,6 +25,8 @@ struct MatvecArgs {
 
 // rpb of the fast matvec when the caller passes 0 (per weight type and shape).
 int default_rpb(WType wt, Epilogue ep, int rows, int cols);
+// Workgroups per CU in the standalone matvec's grid for that shape class (0: as many as can be resident).
+int grid_per_cu(WType wt, Epilogue ep, int rows, int cols);
 // Events the next matvec launch on this thread records at its kernel's start and end (benchmarks: the interval
 // excludes the launch gap).  take_kernel_events() returns and clears them.
 struct KernelEvents {

@@ -25,8 +25,9 @@
 //    a conversion and an FMA per column.  The 8192-wide down rows (KS = 4) keep the float path.
 //  * Row sums are wave64 DPP butterflies (deterministic order); with KS > 1 the slice partials
 //    meet in LDS and are added in slice order.  No atomics anywhere.
-//  * The grid is persistent: min(row blocks, CUs x resident workgroups per CU), but with KS = 1 at
-//    least enough workgroups that none takes more than 64 / R passes.
+//  * The grid: min(row blocks, CUs x the shape class's workgroups per CU (grid_per_cu; by default as
+//    many as can be resident)), but with KS = 1 at least enough workgroups that none takes more than
+//    64 / R passes.
 //
 // Widths with cols % 2048 != 0 or cols/2048 not in {1,4} use matvec_generic, which stages x in LDS.
 #pragma once
@@ -441,8 +442,11 @@ void launch_fast(const MatvecArgs& a, hipStream_t s) {
     const int out_rows = EP == Epilogue::SWIGLU ? a.rows / 2 : a.rows;
     constexpr int ROWS_WG = (4 / KS) * R;
     const int need = (out_rows + ROWS_WG - 1) / ROWS_WG;
-    // Persistent (one wave per SIMD slot), but with KS = 1 no workgroup may take more than kMaxPasses<R> passes.
-    const int grid = std::max(std::min(need, device_cu_count() * occ), KS == 1 ? (need + kMaxPasses<R> - 1) / kMaxPasses<R> : 0);
+    // Workgroups per CU: the shape class's choice, else as many as can be resident; but with KS = 1 no workgroup may
+    // take more than kMaxPasses<R> passes.
+    const int per_cu = grid_per_cu(WT, EP, a.rows, a.cols);
+    const int grid = std::max(std::min(need, device_cu_count() * (per_cu > 0 ? per_cu : occ)),
+                              KS == 1 ? (need + kMaxPasses<R> - 1) / kMaxPasses<R> : 0);
     dispatch(k, grid, 0, s, a);
 }
 

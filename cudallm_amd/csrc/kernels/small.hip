@@ -25,25 +25,42 @@ int device_cu_count() {
     return cache[dev];
 }
 
-// The library's rpb when the caller passes 0, per weight type and shape class, from an rpb sweep of the standalone
-// matvec on MI355X (each class's fastest mean kernel time; e.g. bf16 gate_up 12.97 -> 12.30 us at rpb 1, bf16 down
-// 8.21 -> 7.51 us and int4 down 6.6 -> 5.2 us at rpb 8).  Classes: 0 other, 1 SwiGLU (gate_up), 2 8192 columns
+// The standalone matvec's launch per weight type and shape class, from a joint sweep of rpb and grid size on
+// MI355X (each class's fastest mean kernel time).  Classes: 0 other (qkv, wo), 1 SwiGLU (gate_up), 2 8192 columns
 // (down), 3 vocabulary-sized (>= 65536 rows: lm_head).
+//
+// kDefaultRpb is the rpb used when the caller passes 0.  kGridPerCu caps the grid at that many workgroups per CU
+// (0: as many as can be resident at once).  Smaller grids mean fewer workgroups, each with more passes, so fewer
+// repeats of the input and norm prologue; for bf16 lm_head a grid of 8 per CU, more than can be resident, spreads
+// the last passes more evenly.  Measured effects: bf16 qkv 4.69 -> 4.40 us, gate_up 12.50 -> 12.00, down 7.65 ->
+// 7.50, lm_head 79.8 -> 78.8; int8 gate_up 8.53 -> 7.25; int4 gate_up 7.72 -> 6.68, lm_head 26.50 -> 25.28.
 constexpr int kDefaultRpb[3][4] = {
-    {2, 1, 8, 2},  // bf16
-    {4, 4, 4, 4},  // int8
-    {4, 8, 8, 8},  // int4
+    {1, 1, 2, 2},  // bf16
+    {4, 2, 4, 4},  // int8
+    {4, 4, 8, 4},  // int4
+};
+constexpr int kGridPerCu[3][4] = {
+    {1, 1, 2, 8},  // bf16
+    {0, 1, 0, 0},  // int8
+    {0, 1, 0, 2},  // int4
 };
 
-int default_rpb(WType wt, Epilogue ep, int rows, int cols) {
-    const int cls = ep == Epilogue::SWIGLU ? 1 : cols >= 8192 ? 2 : rows >= 65536 ? 3 : 0;
+namespace {
+int shape_class(Epilogue ep, int rows, int cols) { return ep == Epilogue::SWIGLU ? 1 : cols >= 8192 ? 2 : rows >= 65536 ? 3 : 0; }
+
+int type_index(WType wt) {
     switch (wt) {
-        case WType::BF16: return kDefaultRpb[0][cls];
-        case WType::INT8: return kDefaultRpb[1][cls];
-        case WType::INT4: return kDefaultRpb[2][cls];
+        case WType::BF16: return 0;
+        case WType::INT8: return 1;
+        case WType::INT4: return 2;
     }
     throw ArgError("unknown weight type");
 }
+}  // namespace
+
+int default_rpb(WType wt, Epilogue ep, int rows, int cols) { return kDefaultRpb[type_index(wt)][shape_class(ep, rows, cols)]; }
+
+int grid_per_cu(WType wt, Epilogue ep, int rows, int cols) { return kGridPerCu[type_index(wt)][shape_class(ep, rows, cols)]; }
 
 namespace {
 thread_local KernelEvents t_kernel_events;

@@ -24,9 +24,11 @@ SHAPES = [("qkv", 3072, 2048, "store", True), ("wo", 2048, 2048, "add", False),
           ("gate_up", 16384, 2048, "swiglu", True), ("down", 2048, 8192, "add", False),
           ("lm_head", 128256, 2048, "store", True)]
 RPBS = (1, 2, 4, 8)
-# The library's choice when rpb = 0 (kDefaultRpb / default_rpb in csrc/kernels/small.hip), per weight type and shape
-# class: other, SwiGLU, 8192 columns, >= 65536 rows.
-DEFAULT_RPB = {"bf16": (2, 1, 8, 2), "int8": (4, 4, 4, 4), "int4": (4, 8, 8, 8)}
+# The library's choice when rpb = 0 (kDefaultRpb / default_rpb in csrc/kernels/small.hip), and its grid size in
+# workgroups per CU (kGridPerCu; 0: as many as can be resident), per weight type and shape class: other, SwiGLU, 8192
+# columns, >= 65536 rows.
+DEFAULT_RPB = {"bf16": (1, 1, 2, 2), "int8": (4, 2, 4, 4), "int4": (4, 4, 8, 4)}
+GRID_PER_CU = {"bf16": (1, 1, 2, 8), "int8": (0, 1, 0, 0), "int4": (0, 1, 0, 2)}
 
 
 def default_rpb(wd: str, ep: str, rows: int, cols: int) -> int:

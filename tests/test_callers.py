@@ -153,11 +153,15 @@ def test_default_rpb_matches_the_library():
     src = (Path(__file__).resolve().parents[1] / "cudallm_amd/csrc/kernels/small.hip").read_text()
     body = src[src.index("constexpr int kDefaultRpb[3][4]"):]
     got = {m.group(5): tuple(int(m.group(i)) for i in range(1, 5))
-           for m in re.finditer(r"\{(\d+), (\d+), (\d+), (\d+)\},\s*// (\w+)", body[:300])}
+           for m in re.finditer(r"\{(\d+), (\d+), (\d+), (\d+)\},\s*// (\w+)", body[:body.index("kGridPerCu")])}
     assert got == K.DEFAULT_RPB
+    grid = src[src.index("constexpr int kGridPerCu[3][4]"):]
+    got = {m.group(5): tuple(int(m.group(i)) for i in range(1, 5))
+           for m in re.finditer(r"\{(\d+), (\d+), (\d+), (\d+)\},\s*// (\w+)", grid[:300])}
+    assert got == K.GRID_PER_CU
     assert "ep == Epilogue::SWIGLU ? 1 : cols >= 8192 ? 2 : rows >= 65536 ? 3 : 0" in body
-    assert [K.default_rpb("bf16", ep, r, c) for _, r, c, ep, _ in K.SHAPES] == [2, 2, 1, 8, 2]
-    assert [K.default_rpb("int4", ep, r, c) for _, r, c, ep, _ in K.SHAPES] == [4, 4, 8, 8, 8]
+    assert [K.default_rpb("bf16", ep, r, c) for _, r, c, ep, _ in K.SHAPES] == [1, 1, 1, 2, 2]
+    assert [K.default_rpb("int4", ep, r, c) for _, r, c, ep, _ in K.SHAPES] == [4, 4, 4, 8, 4]
 
 
 def test_shape_winners():
