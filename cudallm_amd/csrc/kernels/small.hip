@@ -31,18 +31,19 @@ int device_cu_count() {
 //
 // kDefaultRpb is the rpb used when the caller passes 0.  kGridPerCu caps the grid at that many workgroups per CU
 // (0: as many as can be resident at once).  Smaller grids mean fewer workgroups, each with more passes, so fewer
-// repeats of the input and norm prologue; for bf16 lm_head a grid of 8 per CU, more than can be resident, spreads
-// the last passes more evenly.  Measured effects: bf16 qkv 4.69 -> 4.40 us, gate_up 12.50 -> 12.00, down 7.65 ->
-// 7.50, lm_head 79.8 -> 78.8; int8 gate_up 8.53 -> 7.25; int4 gate_up 7.72 -> 6.68, lm_head 26.50 -> 25.28.
+// repeats of the input and norm prologue; for bf16 lm_head a grid of 16 workgroups per CU, more than can be resident
+// at once, spreads the last passes more evenly.  Measured effects: bf16 qkv 4.69 -> 4.40 us, gate_up 12.50 -> 12.00,
+// down 7.65 -> 7.50, lm_head 79.8 -> 78.0 (8 per CU) -> 77.0 (16); int8 gate_up 8.53 -> 7.25; int4 gate_up
+// 7.72 -> 6.68, lm_head 26.50 -> 25.28.
 constexpr int kDefaultRpb[3][4] = {
     {1, 1, 2, 2},  // bf16
     {4, 2, 4, 4},  // int8
     {4, 4, 8, 4},  // int4
 };
 constexpr int kGridPerCu[3][4] = {
-    {1, 1, 2, 8},  // bf16
-    {0, 1, 0, 0},  // int8
-    {0, 1, 0, 2},  // int4
+    {1, 1, 2, 16},  // bf16
+    {0, 1, 0, 0},   // int8
+    {0, 1, 0, 2},   // int4
 };
 
 namespace {

@@ -28,7 +28,7 @@ RPBS = (1, 2, 4, 8)
 # workgroups per CU (kGridPerCu; 0: as many as can be resident), per weight type and shape class: other, SwiGLU, 8192
 # columns, >= 65536 rows.
 DEFAULT_RPB = {"bf16": (1, 1, 2, 2), "int8": (4, 2, 4, 4), "int4": (4, 4, 8, 4)}
-GRID_PER_CU = {"bf16": (1, 1, 2, 8), "int8": (0, 1, 0, 0), "int4": (0, 1, 0, 2)}
+GRID_PER_CU = {"bf16": (1, 1, 2, 16), "int8": (0, 1, 0, 0), "int4": (0, 1, 0, 2)}
 
 
 def default_rpb(wd: str, ep: str, rows: int, cols: int) -> int:
