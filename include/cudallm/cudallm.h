@@ -39,7 +39,8 @@ typedef struct {
     int fuse;          /* 0/1: fused RMSNorm / residual / SwiGLU / RoPE+KV-write op order */
     int cuda_graph;    /* 0/1: capture the decode step once as a hipGraph and replay it */
     int max_seq_len;   /* 0 = from file, else a positive multiple of 128 <= the file's value */
-    int matvec_rpb;    /* 0 = default; else 1, 2, 4 or 8 rows per wave per iteration */
+    int matvec_rpb;    /* 0 = the library's per-shape choice; else 1, 2, 4 or 8 rows per wave per iteration (the
+                          grid's workgroups per CU stay the library's per-shape choice either way) */
 } cudallm_options;
 
 /* Reference include/cudallm/cudallm.h:27-32 (10 x int, float, u64 at offset 48). */
