@@ -7,9 +7,13 @@ knobs the default path actually has).
 The knobs (compile-time constants of csrc/kernels/decode.hip):
   CLLM_LOADER_LINES      lines (1 KiB loads) in flight per loader wave            default 16
   CLLM_RING_SLOTS_BF16   LDS ring slots per compute wave, bf16 weights            default 30 (the most that fits)
-  CLLM_RING_SLOTS_QUANT  LDS ring slots per compute wave, int8 / int4 weights     default 22
+  CLLM_RING_SLOTS_QUANT  LDS ring slots per compute wave, int8 weights             default 22
+  CLLM_RING_SLOTS_INT4   LDS ring slots per compute wave, int4 weights             default 20
   CLLM_LM_ROWS_BF16      lm_head rows per unit of work, bf16 weights               default 2
-  CLLM_LM_ROWS_QUANT     lm_head rows per unit of work, int8 / int4 weights        default 8
+  CLLM_LM_ROWS_INT8      lm_head rows per unit of work, int8 weights               default 8
+  CLLM_LM_ROWS_QUANT     lm_head rows per unit of work, int4 weights               default 8
+(the kernel's int4 ring and int8 lm_head units fall back to the QUANT values when their own knob is not given; the
+sweep always gives every knob.)
 ``build`` compiles one library per configuration (one knob moved from the default at a time) into OUT_DIR/NAME/;
 a configuration whose LDS does not fit fails to build and is reported as such.  ``run`` (on the GPU) times each
 library with bench.py's decode leg (CUDALLM_LIB selects the library) and reports the decode kernel's microseconds
@@ -24,11 +28,12 @@ from pathlib import Path
 
 PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
-DEFAULTS = {"CLLM_LOADER_LINES": 16, "CLLM_RING_SLOTS_BF16": 30, "CLLM_RING_SLOTS_QUANT": 22, "CLLM_LM_ROWS_BF16": 2,
-            "CLLM_LM_ROWS_QUANT": 8}
+DEFAULTS = {"CLLM_LOADER_LINES": 16, "CLLM_RING_SLOTS_BF16": 30, "CLLM_RING_SLOTS_QUANT": 22, "CLLM_RING_SLOTS_INT4": 20,
+            "CLLM_LM_ROWS_BF16": 2, "CLLM_LM_ROWS_INT8": 8, "CLLM_LM_ROWS_QUANT": 8}
 # One knob at a time around the defaults.
-MOVES = {"CLLM_LOADER_LINES": (12, 20), "CLLM_RING_SLOTS_BF16": (26,), "CLLM_RING_SLOTS_QUANT": (20, 24),
-         "CLLM_LM_ROWS_BF16": (1, 4), "CLLM_LM_ROWS_QUANT": (2, 4)}
+MOVES = {"CLLM_LOADER_LINES": (12, 20), "CLLM_RING_SLOTS_BF16": (26,), "CLLM_RING_SLOTS_QUANT": (20,),
+         "CLLM_RING_SLOTS_INT4": (18, 22), "CLLM_LM_ROWS_BF16": (1, 4), "CLLM_LM_ROWS_INT8": (4,),
+         "CLLM_LM_ROWS_QUANT": (4,)}
 
 
 def configs() -> dict:
@@ -81,8 +86,9 @@ def run(out_dir: Path, steps: int, warmup: int) -> dict:
 
 
 def report(results: dict) -> str:
-    lines = ["| configuration | loader lines | ring slots bf16 | ring slots int8/int4 | lm_head rows bf16 | "
-             "lm_head rows int8/int4 | bf16 us | int8 us | int4 us |", "|---|---|---|---|---|---|---|---|---|"]
+    lines = ["| configuration | loader lines | ring slots bf16 | ring slots int8 | ring slots int4 | lm_head rows bf16 | "
+             "lm_head rows int8 | lm_head rows int4 | bf16 us | int8 us | int4 us |",
+             "|---|---|---|---|---|---|---|---|---|---|---|"]
     best = {}
     for name, r in results.items():
         c = r["config"]
@@ -95,8 +101,8 @@ def report(results: dict) -> str:
         else:
             cells = ["-", "-", "-"]
         lines.append(f"| {name} | {c['CLLM_LOADER_LINES']} | {c['CLLM_RING_SLOTS_BF16']} | "
-                     f"{c['CLLM_RING_SLOTS_QUANT']} | {c['CLLM_LM_ROWS_BF16']} | {c['CLLM_LM_ROWS_QUANT']} | "
-                     + " | ".join(cells) + " |")
+                     f"{c['CLLM_RING_SLOTS_QUANT']} | {c['CLLM_RING_SLOTS_INT4']} | {c['CLLM_LM_ROWS_BF16']} | "
+                     f"{c['CLLM_LM_ROWS_INT8']} | {c['CLLM_LM_ROWS_QUANT']} | " + " | ".join(cells) + " |")
     lines.append("")
     for wd, (name, v) in sorted(best.items()):
         lines.append(f"* fastest for {wd}: {name} ({v:.1f} us per step)")
