@@ -6,7 +6,7 @@ knobs the default path actually has).
 
 The knobs (compile-time constants of csrc/kernels/decode.hip):
   CLLM_LOADER_LINES      lines (1 KiB loads) in flight per loader wave            default 16
-  CLLM_RING_SLOTS_BF16   LDS ring slots per compute wave, bf16 weights            default 30 (the most that fits)
+  CLLM_RING_SLOTS_BF16   LDS ring slots per compute wave, bf16 weights            default 24 (30 fit)
   CLLM_RING_SLOTS_QUANT  LDS ring slots per compute wave, int8 weights             default 22
   CLLM_RING_SLOTS_INT4   LDS ring slots per compute wave, int4 weights             default 20
   CLLM_LM_ROWS_BF16      lm_head rows per unit of work, bf16 weights               default 2
@@ -28,10 +28,10 @@ from pathlib import Path
 
 PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
-DEFAULTS = {"CLLM_LOADER_LINES": 16, "CLLM_RING_SLOTS_BF16": 30, "CLLM_RING_SLOTS_QUANT": 22, "CLLM_RING_SLOTS_INT4": 20,
+DEFAULTS = {"CLLM_LOADER_LINES": 16, "CLLM_RING_SLOTS_BF16": 24, "CLLM_RING_SLOTS_QUANT": 22, "CLLM_RING_SLOTS_INT4": 20,
             "CLLM_LM_ROWS_BF16": 2, "CLLM_LM_ROWS_INT8": 8, "CLLM_LM_ROWS_QUANT": 8}
 # One knob at a time around the defaults.
-MOVES = {"CLLM_LOADER_LINES": (12, 20), "CLLM_RING_SLOTS_BF16": (26,), "CLLM_RING_SLOTS_QUANT": (20,),
+MOVES = {"CLLM_LOADER_LINES": (12, 20), "CLLM_RING_SLOTS_BF16": (22, 26, 30), "CLLM_RING_SLOTS_QUANT": (20,),
          "CLLM_RING_SLOTS_INT4": (18, 22), "CLLM_LM_ROWS_BF16": (1, 4), "CLLM_LM_ROWS_INT8": (4,),
          "CLLM_LM_ROWS_QUANT": (4,)}
 
