@@ -85,7 +85,8 @@ template <WType WT>
 constexpr int kLmR = WT == WType::BF16 ? CLLM_LM_ROWS_BF16 : WT == WType::INT8 ? CLLM_LM_ROWS_INT8 : CLLM_LM_ROWS_QUANT;  // lm_head rows per unit
 static_assert(walk::kH == H && walk::kInter == INTER && walk::kVocab == VOCAB && walk::kPairs == kPairs,
               "the weight walk and the kernel agree on the shapes");
-static_assert(VOCAB % kLmR<WType::BF16> == 0 && VOCAB % kLmR<WType::INT8> == 0, "lm_head units");
+static_assert(VOCAB % kLmR<WType::BF16> == 0 && VOCAB % kLmR<WType::INT8> == 0 && VOCAB % kLmR<WType::INT4> == 0,
+              "lm_head units");
 
 enum : unsigned { T_QKV = 0, T_ATT_PART = 1, T_ATT = 2, T_XA = 3, T_ACT = 4, T_X = 5 };
 constexpr unsigned T_ARG = NL * kTagStride;
